@@ -1,0 +1,182 @@
+#!/usr/bin/env python3
+"""Forward throughput of the HdcMamba LM on one MI355X.
+
+Default workload: the 24-layer d_model=1024 (d_state 128, 16 heads, chunk 64, vocab 50304,
+tied head) language model forward at B=1, L=32768 in bf16, uniform random token ids and
+random-init weights.  One step = one full forward (embedding, 24 blocks, final norms,
+logits).  Prints ONE JSON line with tokens/s, the roofline of the dominant custom kernel
+(measured with HIP events on the launch stream during the timed steps), per-kernel
+figures, and the CPU oracle's throughput on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def kernel_bytes(cfg, name):
+    """Algorithmic HBM bytes per token of one launch of each custom kernel (bf16 eb=2)."""
+    eb = 2 if cfg["dtype_name"] == "bf16" else 4
+    dm, ds = cfg["d_model"], cfg["d_state"]
+    return {
+        "norm_conv": 2 * dm * eb,          # read x, write x_conv
+        "ssm": 4 * ds * eb,                # read dt, x, b; write y
+        "slot_state": 2 * dm * eb,         # read k, v (pre-pass)
+        "slot_gate": 5 * dm * eb,          # read q, k, v, gate; write gated output
+        "rowln": 2 * (ds + dm) * eb,       # read + write combined row
+    }[name]
+
+
+def cpu_baseline(model, ids_gpu, cfg, budget_s):
+    """Time the CPU oracle on the same weights: all layers at a shorter sequence when the full
+    one would exceed the budget; layers beyond the budget are extrapolated from the mean."""
+    import torch
+
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, int(os.environ.get("HDCM_CPU_THREADS", "16")))
+    torch.set_num_threads(threads)
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    L = min(cfg["L"], 4096)
+    ids = ids_gpu[:1, :L].cpu()
+    bcfg = oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"])
+    n_layers = cfg["n_layers"]
+    F = torch.nn.functional
+    t_start = time.perf_counter()
+    x = F.embedding(ids, sd["embedding.weight"])
+    done, t_layers = 0, 0.0
+    for i in range(n_layers):
+        t0 = time.perf_counter()
+        pre = f"backbone.layers.{i}."
+        x = oracle.block_forward({k[len(pre):]: v for k, v in sd.items() if k.startswith(pre)}, x, bcfg)
+        t_layers += time.perf_counter() - t0
+        done += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    t0 = time.perf_counter()
+    x = F.layer_norm(x, (cfg["d_model"],), sd["backbone.norm_final.weight"], sd["backbone.norm_final.bias"])
+    x = F.layer_norm(x, (cfg["d_model"],), sd["norm_f.weight"], sd["norm_f.bias"])
+    F.linear(x, sd["embedding.weight"])
+    t_tail = time.perf_counter() - t0
+    t_total = t_layers / done * n_layers + t_tail
+    sample = (f"CPU oracle (plain PyTorch, bf16) on the same weights: embedding, {done} of {n_layers} "
+              f"blocks timed (rest extrapolated from their mean), final norms and logits, B=1, L={L}")
+    return {"value": round(L / t_total, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": sample, "cpu_model": _cpu_model(), "seconds_measured": round(time.perf_counter() - t_start, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="lm_c4", choices=["lm_c4", "lm_c3", "block_c2"])
+    ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
+    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one MI355X (got --gpus {args.gpus}, WORLD_SIZE {world}); runs on "
+              "several GPUs are not part of this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from cfgs import WORKLOADS, block_input, lm_input, make_block, make_lm
+    from hdcmamba_amd import _ops
+
+    dev = torch.device("cuda:0")
+    cfg = dict(WORKLOADS[args.workload])
+    cfg["dtype_name"] = "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32"
+    if args.workload.startswith("lm"):
+        model = make_lm(args.workload).to(cfg["dtype"]).to(dev)
+        inp = lm_input(args.workload).to(dev)
+        workload = (f"{cfg['n_layers']}-layer d_model={cfg['d_model']} HdcMamba LM forward, "
+                    f"B={cfg['B']}, L={cfg['L']}")
+    else:
+        model = make_block(args.workload).to(cfg["dtype"]).to(dev)
+        inp = block_input(args.workload).to(dev)
+        workload = f"one HdcMamba block forward, B={cfg['B']}, L={cfg['L']}, d_model={cfg['d_model']}"
+    tokens = cfg["B"] * cfg["L"]
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(inp)
+        torch.cuda.synchronize()
+        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln"}
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            model(inp)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        _ops.timer.active = set()
+    times = _ops.timer.collect()
+    sec = t1 - t0
+    ms_per_step = sec / args.steps * 1e3
+    value = tokens * args.steps / sec
+
+    kernels = {}
+    for name, ms in times.items():
+        us = sum(ms) / len(ms) * 1e3
+        gbs = kernel_bytes(cfg, name) * tokens / (us * 1e-6) / 1e9
+        kernels[name] = {"us": round(us, 2), "launches": len(ms), "GB/s": round(gbs, 1),
+                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = "slot_gate"
+    d = kernels[dom]
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": d["frac_hbm"], "traffic": None,
+                "bytes_per_launch": kernel_bytes(cfg, dom) * tokens}
+    if "slot_state" in kernels:
+        us = kernels["slot_state"]["us"] + kernels["slot_gate"]["us"]
+        gbs = kernel_bytes(cfg, "slot_gate") * tokens / (us * 1e-6) / 1e9
+        kernels["slot_op(state+gate)"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+    cpu = None
+    if args.cpu_baseline == "on" and args.workload.startswith("lm"):
+        cpu = cpu_baseline(model, inp, cfg, args.cpu_budget_s)
+
+    out = {
+        "metric": "forward tokens/sec on 1 MI355X at L=32768; achieved HBM GB/s % of peak",
+        "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": cfg["dtype_name"],
+        "data": "synthetic: uniform random token ids / N(0,1) inputs, random-init weights",
+        "config": {"workload": workload, "d_model": cfg["d_model"], "d_state": cfg["d_state"],
+                   "num_heads": cfg["num_heads"], "chunk": cfg["chunk"], "layers": cfg.get("n_layers", 1),
+                   "vocab": 50304 if args.workload.startswith("lm") else None,
+                   "global_batch": cfg["B"], "seq_len": cfg["L"], "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,19 @@
+"""hdcmamba_amd: the HdcMamba block forward on MI355X (gfx950) HIP kernels.
+
+Public names match the reference package (hdcmamba/__init__.py:1-13).
+"""
+from .model import (
+    FusedNormConv1dFunction,
+    HdcMamba9v3Block,
+    HdcMamba9v3Model,
+    fused_norm_conv1d_trainable,
+)
+from .lm import HdcMambaLM
+
+__all__ = [
+    "HdcMamba9v3Block",
+    "HdcMamba9v3Model",
+    "FusedNormConv1dFunction",
+    "fused_norm_conv1d_trainable",
+    "HdcMambaLM",
+]

@@ -1,0 +1,245 @@
+"""ctypes binding of libhdcmamba_hip.so and tensor-level wrappers.
+
+The C ABI (include/hdcm.h) takes raw device pointers, element strides and a
+hipStream_t.  These wrappers check tensors, allocate outputs and workspaces through
+PyTorch's caching allocator and launch on torch's current stream.  There is no CPU
+or fallback path: a missing library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libhdcmamba_hip.so")
+ABI_VERSION = 1
+
+HDCM_F32, HDCM_BF16 = 0, 1
+_DTYPES = {torch.float32: HDCM_F32, torch.bfloat16: HDCM_BF16}
+
+# name -> (restype, argtypes); mirrors include/hdcm.h
+_PROTOS = {
+    "hdcm_abi_version": (c_int, []),
+    "hdcm_strerror": (ctypes.c_char_p, [c_int]),
+    "hdcm_norm_conv_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_float,
+                                   c_int, c_void_p]),
+    "hdcm_ssm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "hdcm_ssm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                             c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_slot_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
+    "hdcm_slot_state_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t,
+                                    c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_slot_gate_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_float,
+                                   c_void_p, c_size_t, c_void_p, c_int64, c_int64, c_void_p,
+                                   c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_rowln_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                               c_int64, c_float, c_int, c_void_p]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhdcmamba_hip.so (once) and declare its prototypes."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH.name} is not built; run `python -m hdcmamba_amd.build`")
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _PROTOS.items():
+            fn = getattr(h, name)
+            fn.restype, fn.argtypes = res, args
+        if h.hdcm_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH.name} ABI {h.hdcm_abi_version()} != expected {ABI_VERSION}")
+        _lib = h
+    return _lib
+
+
+class HdcmError(RuntimeError):
+    def __init__(self, op: str, code: int):
+        super().__init__(f"{op}: {lib().hdcm_strerror(code).decode()} (status {code})")
+        self.code = code
+
+
+def _check(op: str, code: int) -> None:
+    if code != 0:
+        raise HdcmError(op, code)
+
+
+def _dtype(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("hdcmamba_amd kernels need ROCm GPU tensors; got a tensor on "
+                               f"{t.device} (there is no CPU path)")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _same(t: torch.Tensor, ref: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != ref.dtype:
+        t = t.to(ref.dtype)
+    if t.device != ref.device:
+        raise RuntimeError(f"{name} is on {t.device}, expected {ref.device}")
+    return t.contiguous()
+
+
+def _rows2d(t: torch.Tensor, name: str):
+    """(row stride) of a [..., W] tensor whose rows are uniformly strided."""
+    if t.stride(-1) != 1:
+        raise RuntimeError(f"{name}: last dimension must be contiguous")
+    rs = t.stride(-2) if t.dim() >= 2 else t.shape[-1]
+    # all leading dims must collapse onto rows of stride rs
+    expect = rs
+    for d in range(t.dim() - 2, -1, -1):
+        if t.shape[d] > 1 and t.stride(d) != expect:
+            raise RuntimeError(f"{name}: leading dimensions must collapse to uniformly strided rows")
+        expect *= t.shape[d]
+    return rs
+
+
+# ----------------------------------------------------------------------------- timing hook
+class _Timer:
+    """Records torch.cuda events around named launches (used by bench.py)."""
+
+    def __init__(self):
+        self.active = set()
+        self.events = {}
+
+    def begin(self, name):
+        if name in self.active:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            return ev
+        return None
+
+    def end(self, name, ev0):
+        if ev0 is not None:
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev1.record()
+            self.events.setdefault(name, []).append((ev0, ev1))
+
+    def collect(self):
+        torch.cuda.synchronize()
+        out = {k: [a.elapsed_time(b) for a, b in v] for k, v in self.events.items()}
+        self.events = {}
+        return out
+
+
+timer = _Timer()
+
+
+# ----------------------------------------------------------------------------- wrappers
+def norm_conv(x, ln_w, ln_b, conv_w, conv_b, eps, out=None):
+    """LayerNorm + causal depthwise conv: x [B,L,D] -> out [B,L,D] (x.dtype)."""
+    _on_gpu(x)
+    if x.dim() != 3:
+        raise RuntimeError("norm_conv expects x of shape [B, L, D]")
+    B, L, D = x.shape
+    ln_w = _same(ln_w, x, "ln_w")
+    ln_b = _same(ln_b, x, "ln_b")
+    conv_b = _same(conv_b, x, "conv_b")
+    conv_w = _same(conv_w.reshape(D, 4), x, "conv_w")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    if out is None:
+        out = torch.empty(B, L, D, device=x.device, dtype=x.dtype)
+    ev = timer.begin("norm_conv")
+    _check("hdcm_norm_conv_fwd", lib().hdcm_norm_conv_fwd(
+        x.data_ptr(), x.stride(0), x.stride(1), ln_w.data_ptr(), ln_b.data_ptr(), conv_w.data_ptr(),
+        conv_b.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1), B, L, D, float(eps),
+        _dtype(x), _stream(x)))
+    timer.end("norm_conv", ev)
+    return out
+
+
+def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
+    """Selective scan; writes y [B,L,ds] (may be a column slice of a wider buffer)."""
+    _on_gpu(projs, y)
+    B, L, _ = projs.shape
+    A_log = _same(A_log, projs, "A_log")
+    prs = _rows2d(projs, "projs")
+    yrs = _rows2d(y, "y")
+    nbytes = lib().hdcm_ssm_workspace_bytes(B, L, d_state)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=projs.device)
+    if h0 is not None:
+        h0 = h0.float().contiguous()
+    ev = timer.begin("ssm")
+    _check("hdcm_ssm_fwd", lib().hdcm_ssm_fwd(
+        projs.data_ptr(), prs, A_log.data_ptr(), h0.data_ptr() if h0 is not None else None,
+        y.data_ptr(), yrs, h_final.data_ptr() if h_final is not None else None, ws.data_ptr(), nbytes,
+        B, L, d_state, _dtype(projs), _stream(projs)))
+    timer.end("ssm", ev)
+    return y
+
+
+def slot_workspace(projs, d_model, num_heads, chunk):
+    B, L, _ = projs.shape
+    nbytes = lib().hdcm_slot_workspace_bytes(B, L, d_model, num_heads, chunk, _dtype(projs))
+    if nbytes == 0 and B * L > 0:
+        raise HdcmError("hdcm_slot_workspace_bytes", -3)
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=projs.device)
+
+
+def slot_state(projs, q_col, gamma, d_model, num_heads, chunk, ws, S0=None):
+    """Segment-start states of the slot recurrence into ws."""
+    _on_gpu(projs)
+    B, L, _ = projs.shape
+    gamma = _same(gamma, projs, "gamma")
+    if S0 is not None:
+        S0 = S0.float().contiguous()
+    ev = timer.begin("slot_state")
+    _check("hdcm_slot_state_fwd", lib().hdcm_slot_state_fwd(
+        projs.data_ptr(), _rows2d(projs, "projs"), q_col, gamma.data_ptr(),
+        S0.data_ptr() if S0 is not None else None, ws.data_ptr(), ws.numel(), B, L, d_model,
+        num_heads, chunk, _dtype(projs), _stream(projs)))
+    timer.end("slot_state", ev)
+    return ws
+
+
+def slot_gate(projs, q_col, gamma, gn_w, gn_b, gn_eps, ws, out, out_col, d_model, num_heads, chunk,
+              S_final=None):
+    """Slot memory + GroupNorm + sigmoid gate into out[..., out_col:out_col+d_model]."""
+    _on_gpu(projs, out)
+    B, L, _ = projs.shape
+    gamma = _same(gamma, projs, "gamma")
+    gn_w = _same(gn_w, projs, "gn_w")
+    gn_b = _same(gn_b, projs, "gn_b")
+    ev = timer.begin("slot_gate")
+    _check("hdcm_slot_gate_fwd", lib().hdcm_slot_gate_fwd(
+        projs.data_ptr(), _rows2d(projs, "projs"), q_col, gamma.data_ptr(), gn_w.data_ptr(),
+        gn_b.data_ptr(), float(gn_eps), ws.data_ptr(), ws.numel(), out.data_ptr(), _rows2d(out, "out"),
+        out_col, S_final.data_ptr() if S_final is not None else None, B, L, d_model, num_heads, chunk,
+        _dtype(projs), _stream(projs)))
+    timer.end("slot_gate", ev)
+    return out
+
+
+def layer_norm(x, w=None, b=None, eps=1e-5, out=None):
+    """Row LayerNorm over the last dim (fp32 statistics); in-place when out is x."""
+    _on_gpu(x)
+    W = x.shape[-1]
+    if w is not None:
+        w = _same(w, x, "w")
+        b = _same(b, x, "b")
+    if out is None:
+        out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    rows = x.numel() // W if W else 0
+    ev = timer.begin("rowln")
+    _check("hdcm_rowln_fwd", lib().hdcm_rowln_fwd(
+        x.data_ptr(), _rows2d(x, "x"), out.data_ptr(), _rows2d(out, "out"),
+        w.data_ptr() if w is not None else None, b.data_ptr() if b is not None else None,
+        rows, W, float(eps), _dtype(x), _stream(x)))
+    timer.end("rowln", ev)
+    return out

@@ -1,0 +1,180 @@
+// Shared device helpers for the HdcMamba gfx950 kernels.
+//
+// Element types: activations are either fp32 (`float`) or bf16 stored as raw
+// `uint16_t` bits.  All arithmetic is fp32; bf16 values are produced with
+// round-to-nearest-even, the rounding torch and the MFMA operand path use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hdcm.h"
+
+namespace hdcm {
+
+typedef uint16_t bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ float to_f(T v);
+template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f<bf16_t>(bf16_t v) { return bf2f(v); }
+
+template <typename T> __device__ __forceinline__ T from_f(float v);
+template <> __device__ __forceinline__ float from_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f<bf16_t>(float v) { return f2bf(v); }
+
+// Round to the storage type and back (identity for fp32).
+template <typename T> __device__ __forceinline__ float rnd(float v) { return to_f<T>(from_f<T>(v)); }
+
+// Elements per 16-byte vector.
+template <typename T> struct Vec { static constexpr int N = 16 / sizeof(T); };
+
+// ------------------------------------------------------- 16-byte vector I/O
+template <typename T> __device__ __forceinline__ void load16(const T* p, float* out);
+template <> __device__ __forceinline__ void load16<float>(const float* p, float* out) {
+  float4 v = *reinterpret_cast<const float4*>(p);
+  out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+}
+template <> __device__ __forceinline__ void load16<bf16_t>(const bf16_t* p, float* out) {
+  uint4 v = *reinterpret_cast<const uint4*>(p);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+template <typename T> __device__ __forceinline__ void store16(T* p, const float* in);
+template <> __device__ __forceinline__ void store16<float>(float* p, const float* in) {
+  *reinterpret_cast<float4*>(p) = make_float4(in[0], in[1], in[2], in[3]);
+}
+template <> __device__ __forceinline__ void store16<bf16_t>(bf16_t* p, const float* in) {
+  uint4 v;
+  v.x = (uint32_t)f2bf(in[0]) | ((uint32_t)f2bf(in[1]) << 16);
+  v.y = (uint32_t)f2bf(in[2]) | ((uint32_t)f2bf(in[3]) << 16);
+  v.z = (uint32_t)f2bf(in[4]) | ((uint32_t)f2bf(in[5]) << 16);
+  v.w = (uint32_t)f2bf(in[6]) | ((uint32_t)f2bf(in[7]) << 16);
+  *reinterpret_cast<uint4*>(p) = v;
+}
+
+// Raw (unconverted) 16-byte loads, for staging data whose conversion happens later.
+__device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+
+template <typename T> __device__ __forceinline__ void unpack16(uint4 v, float* out);
+template <> __device__ __forceinline__ void unpack16<float>(uint4 v, float* out) {
+  out[0] = __uint_as_float(v.x); out[1] = __uint_as_float(v.y);
+  out[2] = __uint_as_float(v.z); out[3] = __uint_as_float(v.w);
+}
+template <> __device__ __forceinline__ void unpack16<bf16_t>(uint4 v, float* out) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// ------------------------------------------------------------ wave reductions
+// Butterfly over all 64 lanes; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Sum over the four lanes l, l^16, l^32, l^48 (the row groups of an MFMA C/D tile).
+__device__ __forceinline__ float quad_group_sum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// ------------------------------------------------------------- MFMA fragments
+// A 16x16 MFMA tile step contracts K=32.  A lane owns 8 contraction slots s=0..7 of
+// one row (A operand) or column (B operand).  For bf16 the 8 slots feed one
+// v_mfma_f32_16x16x32_bf16; for fp32 they feed eight v_mfma_f32_16x16x4_f32, slot s
+// going to the s-th instruction.  Either way lane group g=lane/16 and slot s name
+// the same contraction index in the A and the B fragment, so any bijection
+// (g,s) -> k used consistently for both operands yields the full K=32 sum.
+//
+// Output layout (both instruction families): lane l holds D[4*(l/16)+r][l%16], r=0..3.
+template <typename T> struct Frag;
+template <> struct Frag<bf16_t> { bf16x8_t v; };
+template <> struct Frag<float> { float v[8]; };
+
+__device__ __forceinline__ f32x4_t mma(const Frag<bf16_t>& a, const Frag<bf16_t>& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mma(const Frag<float>& a, const Frag<float>& b, f32x4_t c) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[s], b.v[s], c, 0, 0, 0);
+  return c;
+}
+
+// 8 consecutive elements (slots 0..7) from LDS.
+__device__ __forceinline__ void frag_load8(Frag<bf16_t>& f, const bf16_t* p) {
+  f.v = *reinterpret_cast<const bf16x8_t*>(p);
+}
+__device__ __forceinline__ void frag_load8(Frag<float>& f, const float* p) {
+  float4 a = *reinterpret_cast<const float4*>(p);
+  float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f.v[0] = a.x; f.v[1] = a.y; f.v[2] = a.z; f.v[3] = a.w;
+  f.v[4] = b.x; f.v[5] = b.y; f.v[6] = b.z; f.v[7] = b.w;
+}
+// Slots 0..3 from p0 and slots 4..7 from p1 (4 consecutive elements each).
+__device__ __forceinline__ void frag_load4x2(Frag<bf16_t>& f, const bf16_t* p0, const bf16_t* p1) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t a = *reinterpret_cast<const bf16x4_t*>(p0);
+  bf16x4_t b = *reinterpret_cast<const bf16x4_t*>(p1);
+  f.v = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ void frag_load4x2(Frag<float>& f, const float* p0, const float* p1) {
+  float4 a = *reinterpret_cast<const float4*>(p0);
+  float4 b = *reinterpret_cast<const float4*>(p1);
+  f.v[0] = a.x; f.v[1] = a.y; f.v[2] = a.z; f.v[3] = a.w;
+  f.v[4] = b.x; f.v[5] = b.y; f.v[6] = b.z; f.v[7] = b.w;
+}
+// Build a fragment from 8 fp32 values, rounding to the operand type.
+__device__ __forceinline__ void frag_from_f32(Frag<bf16_t>& f, const float* x) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) f.v[s] = __builtin_bit_cast(__bf16, f2bf(x[s]));
+}
+__device__ __forceinline__ void frag_from_f32(Frag<float>& f, const float* x) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) f.v[s] = x[s];
+}
+
+// Host-side dtype mapping.
+template <typename T> struct DtypeOf;
+template <> struct DtypeOf<float> { static constexpr int value = HDCM_F32; };
+template <> struct DtypeOf<bf16_t> { static constexpr int value = HDCM_BF16; };
+
+}  // namespace hdcm
+
+// ------------------------------------------------------------ host-side checks
+#define HDCM_CHECK_ARG(cond, code) \
+  do {                             \
+    if (!(cond)) return (code);    \
+  } while (0)
+
+static inline bool hdcm_aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+static inline int hdcm_elt_size(int dtype) { return dtype == HDCM_F32 ? 4 : 2; }
+
+static inline int hdcm_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? HDCM_OK : HDCM_ELAUNCH;
+}

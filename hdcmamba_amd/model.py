@@ -1,0 +1,139 @@
+"""HdcMamba block and model on MI355X: the reference module surface over HIP kernels.
+
+Drop-in for hdcmamba/model.py of N01N9/hdcmamba: the class and function names,
+constructor signatures, parameter/buffer names and shapes, and the order in which
+construction consumes the global RNG (so ``torch.manual_seed(s)`` followed by
+construction yields the same weights) are those of the reference.  The forward of a
+block runs, per layer:
+
+    norm_conv (HIP)  ->  in_proj (hipBLASLt GEMM)  ->  ssm (HIP) and slot+gate (HIP)
+    writing one `combined` row buffer  ->  row LayerNorm (HIP, in place)
+    ->  out_proj GEMM with the residual fused (addmm)
+
+Intended semantics are computed (see the oracle's docstring for the reference kernel
+defects that are not reproduced).  Only GPU tensors are accepted; there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _ops
+
+__all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
+           "fused_norm_conv1d_trainable"]
+
+
+class FusedNormConv1dFunction(torch.autograd.Function):
+    """LayerNorm + causal depthwise conv1d (width 4), forward on the HIP kernel.
+
+    Same ``apply(x, norm_weight, norm_bias, conv_weight[D,4], conv_bias, eps)`` signature
+    as hdcmamba/model.py:126-146.  Only the forward is built.
+    """
+
+    @staticmethod
+    def forward(ctx, x, norm_weight, norm_bias, conv_weight, conv_bias, eps):
+        return _ops.norm_conv(x, norm_weight, norm_bias, conv_weight, conv_bias, eps)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        raise NotImplementedError("hdcmamba_amd builds the forward path only; "
+                                  "FusedNormConv1dFunction has no backward kernel")
+
+
+def fused_norm_conv1d_trainable(x, norm_layer, conv_layer):
+    """hdcmamba/model.py:168-172: weights cast to x.dtype, conv weight squeezed to [D,4]."""
+    return FusedNormConv1dFunction.apply(
+        x, norm_layer.weight.to(x.dtype), norm_layer.bias.to(x.dtype),
+        conv_layer.weight.squeeze(1).to(x.dtype), conv_layer.bias.to(x.dtype), norm_layer.eps)
+
+
+class HdcMamba9v3Block(nn.Module):
+    """SSM + slot-memory block (hdcmamba/model.py:300-394).
+
+    ``forward(x[B,L,d_model]) -> (y[B,L,d_model], None)``.  L is left-padded with zero
+    rows to a multiple of ``chunk_size`` and the pad is sliced off the output
+    (model.py:388-389,394).
+    """
+
+    def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256):
+        super().__init__()
+        self.d_model, self.d_state = d_model, d_state
+        self.num_heads, self.chunk_size = num_heads, chunk_size
+        self.head_dim = d_model // num_heads
+        proj = 3 * d_state + 4 * d_model
+
+        # Construction order fixes the RNG stream (model.py:306-327).
+        self.norm = nn.LayerNorm(d_model)
+        self.conv1d = nn.Conv1d(d_model, d_model, kernel_size=4, groups=d_model, padding=3, bias=True)
+        with torch.no_grad():
+            nn.init.normal_(self.conv1d.weight, std=0.02)
+            self.conv1d.weight[:, 0, -1] += 1.0  # start close to the identity tap
+            self.conv1d.bias.zero_()
+        self.in_proj = nn.Linear(d_model, proj, bias=True)
+        with torch.no_grad():
+            lo, hi = 0.001, 0.1  # dt = softplus(bias) starts uniform in [lo, hi]
+            dt0 = torch.rand(d_state) * (hi - lo) + lo
+            self.in_proj.bias[:d_state] = torch.log(torch.exp(dt0) - 1.0)
+            q0, gate0 = 3 * d_state, 3 * d_state + 3 * d_model
+            nn.init.xavier_uniform_(self.in_proj.weight[q0:gate0])
+            self.in_proj.bias[gate0:].fill_(1.0)
+        self.A_log = nn.Parameter(torch.log(torch.linspace(0.99, 0.9999, d_state)))
+        self.decay_log = nn.Parameter(torch.log(torch.full((num_heads,), 0.05)))
+        self.out_proj = nn.Linear(d_state + d_model, d_model, bias=False)
+        self.group_norm = nn.GroupNorm(num_heads, d_model)
+        self.register_buffer("gamma_buf", torch.exp(-F.softplus(self.decay_log)))
+
+    def _inner_forward(self, x):
+        """Block body on a chunk-aligned [B,L,dm] input; returns out_proj(LN(combined)) + x."""
+        B, L, dm = x.shape
+        ds, H, C = self.d_state, self.num_heads, self.chunk_size
+        dtype = x.dtype
+        x_conv = fused_norm_conv1d_trainable(x, self.norm, self.conv1d)
+        projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
+        combined = torch.empty(B, L, ds + dm, device=x.device, dtype=dtype)
+        _ops.ssm(projs, self.A_log, ds, combined[..., :ds])
+        gamma = self.gamma_buf.to(dtype)
+        q_col = 3 * ds
+        ws = _ops.slot_workspace(projs, dm, H, C)
+        _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
+        _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
+                       combined, ds, dm, H, C)
+        _ops.layer_norm(combined, eps=1e-5, out=combined)
+        out = torch.addmm(x.reshape(B * L, dm), combined.view(B * L, ds + dm),
+                          self.out_proj.weight.to(dtype).t())
+        return out.view(B, L, dm)
+
+    def forward(self, x):
+        _ops._on_gpu(x)
+        B, L_in, _ = x.shape
+        pad = (self.chunk_size - (L_in % self.chunk_size)) % self.chunk_size
+        if pad > 0:
+            x = F.pad(x, (0, 0, pad, 0))
+        if self.training:
+            with torch.no_grad():
+                self.gamma_buf.copy_(torch.exp(-F.softplus(self.decay_log)))
+        y = self._inner_forward(x.contiguous())
+        return y[:, pad:, :], None
+
+
+class HdcMamba9v3Model(nn.Module):
+    """Stack of blocks plus a final LayerNorm (hdcmamba/model.py:396-404).
+
+    ``num_slots`` is accepted and unused, as in the reference.  ``chunk_size`` is an
+    added keyword; its default 256 is the value the reference hard-codes.
+    """
+
+    def __init__(self, d_model, n_layers, d_state, num_slots, num_heads=8, chunk_size=256):
+        super().__init__()
+        self.layers = nn.ModuleList([
+            HdcMamba9v3Block(d_model=d_model, d_state=d_state, num_heads=num_heads, chunk_size=chunk_size)
+            for _ in range(n_layers)])
+        self.norm_final = nn.LayerNorm(d_model)
+
+    def forward(self, x):
+        for layer in self.layers:
+            x, _ = layer(x)
+        return _ops.layer_norm(x.contiguous(), self.norm_final.weight, self.norm_final.bias,
+                               self.norm_final.eps)

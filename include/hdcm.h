@@ -1,0 +1,124 @@
+/*
+ * hdcm.h -- C ABI of libhdcmamba_hip.so, the gfx950 (MI355X) kernels of the
+ * HdcMamba block forward.
+ *
+ * Conventions
+ *  - Every pointer is device memory owned by the caller.  The library never
+ *    allocates, frees or synchronises; scratch space comes in through `ws`.
+ *  - Activation tensors are row-major with unit element stride inside a row.
+ *    Row strides are given in elements.  Rows of a [B,L,*] tensor are indexed
+ *    b*L + t unless a separate batch stride is taken.  Every pointer and every
+ *    row stride must keep rows 16-byte aligned (128-bit loads and stores).
+ *  - `dtype` (hdcm_dtype) applies to every activation and parameter pointer of
+ *    a call; recurrent states (`h0`, `h_final`, `S0`, `S_final`) are fp32.
+ *  - `stream` is a hipStream_t; all work is ordered on it.  Calls on distinct
+ *    streams with distinct buffers may run concurrently.
+ *  - Functions return an hdcm_status.  Arguments are validated before any
+ *    HIP call, so a failed validation has no side effect.
+ *
+ * Reference: N01N9/hdcmamba launches Triton kernels from Python
+ * (hdcmamba/model.py); each entry point below names the launch it replaces.
+ */
+#ifndef HDCM_H_
+#define HDCM_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum { HDCM_F32 = 0, HDCM_BF16 = 1 } hdcm_dtype;
+
+typedef enum {
+  HDCM_OK = 0,
+  HDCM_EINVAL = -1,       /* null pointer, bad shape or stride */
+  HDCM_EALIGN = -2,       /* pointer or row stride not 16-byte aligned */
+  HDCM_EUNSUPPORTED = -3, /* valid but not built: dtype/head_dim/chunk combination */
+  HDCM_ELAUNCH = -4,      /* a HIP launch reported an error */
+  HDCM_EWORKSPACE = -5    /* workspace missing or smaller than required */
+} hdcm_status;
+
+#define HDCM_ABI_VERSION 1
+
+int hdcm_abi_version(void);
+const char* hdcm_strerror(int status);
+
+/*
+ * LayerNorm over D (biased variance, eps) followed by the causal depthwise
+ * conv of width 4: out[t] = sum_k LN(x)[t-3+k] * conv_w[:,k] + conv_b, with
+ * LN rows t<0 equal to ln_b (LayerNorm of a zero row).
+ * x, out: [B,L,D]; ln_w, ln_b, conv_b: [D]; conv_w: [D,4] contiguous.
+ * Needs D % (16/elt_size) == 0 and D/(16/elt_size) <= 768 (bf16 D <= 6144,
+ * fp32 D <= 3072).
+ * Replaces: FusedNormConv1dFunction.forward -> _fused_norm_conv_fwd_kernel
+ *           (hdcmamba/model.py:128-146, kernel model.py:22-72).
+ */
+int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t x_row_stride,
+                       const void* ln_w, const void* ln_b, const void* conv_w, const void* conv_b,
+                       void* out, int64_t out_batch_stride, int64_t out_row_stride,
+                       int64_t B, int64_t L, int64_t D, float eps, int dtype, void* stream);
+
+/*
+ * Diagonal selective scan over ds channels.  For row (b,t) of projs, columns
+ * [0,ds) hold dt_raw, [ds,2ds) x and [2ds,3ds) b.  With dt = softplus(dt_raw)
+ * (threshold 20) and A = -exp(A_log): h_t = h_{t-1} * exp(dt*A) + dt*b*x,
+ * y[b,t,:] = h_t.  h0 [B,ds] fp32 (NULL = zeros); h_final [B,ds] fp32 or NULL.
+ * y rows may alias the first ds columns of the `combined` buffer.
+ * Replaces: _ssm_intra_v2 + _ssm_scan_v2 + _ssm_inter_v2 launches and the
+ *           y_ssm copy into `combined` (hdcmamba/model.py:345-363, 294-295).
+ */
+size_t hdcm_ssm_workspace_bytes(int64_t B, int64_t L, int64_t ds);
+int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
+                 const float* h0, void* y, int64_t y_row_stride, float* h_final,
+                 void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds,
+                 int dtype, void* stream);
+
+/*
+ * Slot memory (per-head decayed linear attention, feature map elu+1) in two
+ * calls sharing one workspace.  q, k, v and gate are the column blocks
+ * [q_col, q_col+dm), [+dm, +2dm), [+2dm, +3dm), [+3dm, +4dm) of projs; head h
+ * owns columns h*hd..h*hd+hd-1 of each block, hd = dm/H.  gamma [H] is the
+ * per-head decay.  With chunk size C the weight of (t, j<=t) is gamma^(t-j)
+ * inside t's chunk and gamma^(t-j-1) across chunks.
+ *
+ * hdcm_slot_state_fwd computes the chunk-boundary state at the start of every
+ * sequence segment into ws (S0 [B,H,hd,hd] fp32 = state before row 0, or NULL).
+ * hdcm_slot_gate_fwd then produces, per (token, head), GroupNorm over hd
+ * (gn_eps, affine gn_w/gn_b [dm]) times sigmoid(gate), written to columns
+ * [out_col, out_col+dm) of `out`; S_final [B,H,hd,hd] fp32 (or NULL) receives
+ * the state after row L-1 (L must then be a multiple of C).
+ * Needs hd in {32,64,96}; C a power of two dividing the row tile (64 rows
+ * for bf16, 32 for fp32) or a multiple of it; L a multiple of C.
+ * Replaces: _slot_all_fused launch (hdcmamba/model.py:366-371, kernel
+ *           model.py:236-272) and the slot part of _fused_gnorm_gate_cat_kernel
+ *           (model.py:375-380, kernel model.py:274-293).
+ */
+size_t hdcm_slot_workspace_bytes(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C,
+                                 int dtype);
+int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col,
+                        const void* gamma, const float* S0, void* ws, size_t ws_bytes,
+                        int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C,
+                        int dtype, void* stream);
+int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col,
+                       const void* gamma, const void* gn_w, const void* gn_b, float gn_eps,
+                       const void* ws, size_t ws_bytes, void* out, int64_t out_row_stride,
+                       int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t dm,
+                       int64_t H, int64_t C, int dtype, void* stream);
+
+/*
+ * Row LayerNorm over `width` columns, fp32 statistics, optional affine
+ * (w, b may be NULL).  in and out may be the same buffer.
+ * Replaces: F.layer_norm(combined.float(), (ds+dm,)).to(dtype)
+ *           (hdcmamba/model.py:382) and norm_final (model.py:400,404).
+ */
+int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out_row_stride,
+                   const void* w, const void* b, int64_t rows, int64_t width, float eps,
+                   int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HDCM_H_ */

@@ -1,0 +1,427 @@
+"""CPU oracle for the HdcMamba block forward -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in plain PyTorch on the CPU, what the reference computes on
+its forward path (N01N9/hdcmamba, ``hdcmamba/model.py``).  It is the checker the
+HIP kernels are compared against; only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s CPU-baseline leg may import it.  The product package
+(``hdcmamba_amd``) never imports it and has no CPU fallback.
+
+Two semantics are provided:
+
+* ``"intended"`` (default): what the reference module means to compute.  Every
+  internal quantity stays fp32 and is rounded to the activation dtype only where a
+  tensor is materialised (projs, the concatenated ``combined`` row, the block
+  output).  Operands of the reference's ``tl.dot`` calls are rounded to the
+  activation dtype exactly where the reference rounds them (model.py:263,265,268,
+  271), which is a no-op in fp32.
+* ``"faithful"``: additionally reproduces the reference kernels' deterministic
+  defects -- the gate/y_ssm launch strides (model.py:377), the 128-position chunk
+  map in the gate kernel (model.py:288), the constant-one padding features when
+  ``head_dim`` is not a power of two >= 64 (model.py:245-262,290) and the bf16
+  rounding of SSM intermediates and of the gated slot output even for fp32
+  inputs (model.py:196-198,209,233,293).  Chunk sizes above 128 read memory the
+  reference never wrote (model.py:17,245-246) and are rejected.
+
+Parity status of each function (how it is pinned, see tests/test_oracle_*.py):
+
+* ``norm_conv``      -- pinned: F.layer_norm + F.conv1d library routines, identity-tap KAT.
+* ``ssm_sequential`` -- pinned: closed form for constant inputs, brute-force Python loop.
+* ``ssm_chunked``    -- pinned: equals ``ssm_sequential`` for several chunk sizes.
+* ``slot_sequential``-- pinned: hand-computed two-token KAT of the cross-chunk rule,
+  C=L reduces to masked decayed attention, gamma=1 reduces to a cumulative sum.
+* ``slot_chunked``   -- pinned: equals ``slot_sequential`` (fp32) for several chunk sizes.
+* ``gnorm_gate``     -- pinned: F.group_norm per token + torch.sigmoid.
+* ``rowln``          -- pinned: F.layer_norm.
+* faithful-mode address maps (B1-B3, B5) -- pinned only by hand-computed index
+  KATs restated from the launch arguments; parity with the reference's GPU
+  execution is unpinned (the reference needs a CUDA GPU and Triton).
+* constructor RNG order -- pinned by the fixture in tests/golden (see its script).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "BlockCfg", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
+    "slot_sequential", "slot_chunked", "gnorm_gate", "rowln", "block_forward",
+    "model_forward", "lm_forward", "init_block_params",
+]
+
+
+@dataclass(frozen=True)
+class BlockCfg:
+    d_model: int
+    d_state: int
+    num_heads: int
+    chunk_size: int
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.num_heads
+
+    @property
+    def proj_width(self) -> int:
+        return 3 * self.d_state + 4 * self.d_model
+
+
+def _rnd(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Round fp32 values to ``dtype`` and back (no-op for fp32)."""
+    return t.to(dtype).float()
+
+
+def softplus20(x: torch.Tensor) -> torch.Tensor:
+    """softplus with threshold 20 as written at model.py:192 and 229: log(1+exp(x))."""
+    return torch.where(x > 20.0, x, torch.log(1.0 + torch.exp(x)))
+
+
+def phi(z: torch.Tensor) -> torch.Tensor:
+    """Feature map elu(z)+1 as written at model.py:261-262."""
+    return torch.where(z > 0, z + 1.0, torch.exp(z))
+
+
+# --------------------------------------------------------------------------------------
+# LayerNorm + causal depthwise conv (model.py:22-72, 126-146, 168-172)
+# --------------------------------------------------------------------------------------
+def norm_conv(x, ln_w, ln_b, conv_w, conv_b, eps):
+    """out[t] = sum_k u[t-3+k] * w[:,k] + b, u = LayerNorm(x) with biased variance.
+
+    Rows t<0 are LayerNorm of a zero row, i.e. the LN bias (model.py:47-54).
+    ``conv_w`` is [D,4] (``conv1d.weight.squeeze(1)``).  Math in fp32, output in x.dtype
+    (model.py:62-71).
+    """
+    dtype = x.dtype
+    xf = x.float()
+    B, L, D = xf.shape
+    w = ln_w.to(dtype).float()
+    b = ln_b.to(dtype).float()
+    cw = conv_w.to(dtype).float()
+    cb = conv_b.to(dtype).float()
+    mean = xf.mean(-1, keepdim=True)
+    xc = xf - mean
+    var = (xc * xc).mean(-1, keepdim=True)
+    u = xc * torch.rsqrt(var + eps) * w + b
+    up = torch.cat([b.expand(B, 3, D), u], dim=1)
+    out = (up[:, 0:L] * cw[:, 0] + up[:, 1:L + 1] * cw[:, 1]
+           + up[:, 2:L + 2] * cw[:, 2] + up[:, 3:L + 3] * cw[:, 3] + cb)
+    return out.to(dtype)
+
+
+# --------------------------------------------------------------------------------------
+# Selective scan over d_state channels (model.py:175-233)
+# --------------------------------------------------------------------------------------
+def _ssm_inputs(projs, A_log, ds):
+    dt_raw = projs[..., 0:ds].float()
+    xs = projs[..., ds:2 * ds].float()
+    bs = projs[..., 2 * ds:3 * ds].float()
+    A = -torch.exp(A_log.float())
+    dt = softplus20(dt_raw)
+    return dt, dt * A, dt * bs * xs  # dt, log-decay, input term (model.py:192-195)
+
+
+def ssm_sequential(projs, A_log, ds, h0=None):
+    """Direct per-token recurrence h_t = h_{t-1} * exp(ld_t) + dt_t*b_t*x_t, y_t = h_t.
+
+    Returns (y fp32 [B,L,ds], h_final fp32 [B,ds]).
+    """
+    _, ld, u = _ssm_inputs(projs, A_log, ds)
+    B, L, _ = ld.shape
+    h = torch.zeros(B, ds) if h0 is None else h0.float().clone()
+    y = torch.empty(B, L, ds)
+    for t in range(L):
+        h = h * torch.exp(ld[:, t]) + u[:, t]
+        y[:, t] = h
+    return y, h
+
+
+def ssm_chunked(projs, A_log, ds, C, dtype=torch.float32, semantics="intended", h0=None):
+    """Chunked form of the scan as the reference launches it (model.py:345-363).
+
+    intra (model.py:187-198): per chunk, h from 0; y_intra, last state, sum of log decays.
+    scan  (model.py:207-212): G[n] = carried state before chunk n.
+    inter (model.py:226-233): y = y_intra + G[n] * exp(cumsum(ld)).
+    Faithful mode rounds y_intra/last/sum(ld)/G and y to bf16 as the kernels store them.
+    Returns (y fp32 [B,L,ds], h_final fp32 [B,ds]).
+    """
+    _, ld, u = _ssm_inputs(projs, A_log, ds)
+    B, L, _ = ld.shape
+    assert L % C == 0
+    N = L // C
+    ld = ld.view(B, N, C, ds)
+    u = u.view(B, N, C, ds)
+    bf = (lambda t: _rnd(t, torch.bfloat16)) if semantics == "faithful" else (lambda t: t)
+    acc = torch.zeros(B, N, ds)
+    sld = torch.zeros(B, N, ds)
+    y_intra = torch.empty(B, N, C, ds)
+    for c in range(C):
+        sld = sld + ld[:, :, c]
+        acc = acc * torch.exp(ld[:, :, c]) + u[:, :, c]
+        y_intra[:, :, c] = acc
+    y_intra, last, sld = bf(y_intra), bf(acc), bf(sld)
+    state = torch.zeros(B, ds) if h0 is None else h0.float().clone()
+    G = torch.empty(B, N, ds)
+    for n in range(N):
+        G[:, n] = bf(state)
+        state = state * torch.exp(sld[:, n]) + last[:, n]
+    cum = torch.zeros(B, N, ds)
+    y = torch.empty(B, N, C, ds)
+    for c in range(C):
+        cum = cum + ld[:, :, c]
+        y[:, :, c] = bf(y_intra[:, :, c] + G * torch.exp(cum))
+    return y.view(B, L, ds), state
+
+
+# --------------------------------------------------------------------------------------
+# Slot memory: per-head decayed linear attention (model.py:236-272)
+# --------------------------------------------------------------------------------------
+def _slot_qkv(projs, dm, ds, H):
+    B, L, _ = projs.shape
+    hd = dm // H
+    off = 3 * ds
+    q = projs[..., off:off + dm].float().view(B, L, H, hd)
+    k = projs[..., off + dm:off + 2 * dm].float().view(B, L, H, hd)
+    v = projs[..., off + 2 * dm:off + 3 * dm].float().view(B, L, H, hd)
+    return q, k, v
+
+
+def slot_sequential(projs, gamma, dm, ds, H, C):
+    """Brute-force y_t = sum_{j<=t} w(t,j) (phi(q_t).phi(k_j)) v_j, fp32, small inputs only.
+
+    w(t,j) = gamma^(t-j) when j is in t's chunk and gamma^(t-j-1) otherwise
+    (model.py:265 for the intra-chunk part, model.py:267-268 + 271-272 for the carry).
+    Returns y fp32 [B,L,H,hd].
+    """
+    q, k, v = _slot_qkv(projs, dm, ds, H)
+    q, k = phi(q), phi(k)
+    B, L, _, hd = q.shape
+    g = gamma.float()
+    y = torch.zeros(B, L, H, hd)
+    for t in range(L):
+        for j in range(t + 1):
+            e = (t - j) - (0 if t // C == j // C else 1)
+            w = g ** e  # [H]
+            s = (q[:, t] * k[:, j]).sum(-1) * w  # [B,H]
+            y[:, t] += s[..., None] * v[:, j]
+    return y
+
+
+def slot_chunked(projs, gamma, dm, ds, H, C, dtype=torch.float32, semantics="intended", S0=None):
+    """Chunked slot recurrence exactly as model.py:254-272 orders it.
+
+    Operands of each dot are rounded to ``dtype`` where the reference rounds them.
+    In faithful mode, heads with head_dim below max(64, next_pow2(head_dim)) get the
+    reference's constant-one padding features (masked loads of 0 map to phi(0)=1).
+    Returns (y fp32 [B,L,H,hd], running state fp32 [B,H,hdk,hd]).
+    """
+    q, k, v = _slot_qkv(projs, dm, ds, H)
+    B, L, _, hd = q.shape
+    assert L % C == 0
+    N = L // C
+    qf = _rnd(phi(q), dtype)
+    kf = _rnd(phi(k), dtype)
+    if semantics == "faithful":
+        blk = max(64, 1 << (hd - 1).bit_length())
+        if blk > hd:
+            ones = torch.ones(B, L, H, blk - hd)
+            qf = torch.cat([qf, ones], -1)
+            kf = torch.cat([kf, ones], -1)
+    hk = qf.shape[-1]
+    # [B,H,N,C,*]
+    qf = qf.view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    kf = kf.view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    vv = v.view(B, N, C, H, hd).permute(0, 3, 1, 2, 4)
+    lg = torch.log(gamma.float()).view(1, H, 1, 1, 1)
+    idx = torch.arange(C, dtype=torch.float32)
+    diff = idx[:, None] - idx[None, :]
+    causal = diff >= 0
+    decay = torch.exp(diff * lg)  # [1,H,1,C,C]
+    scores = qf @ kf.transpose(-1, -2)
+    scores = _rnd(torch.where(causal, scores * decay, torch.zeros(())), dtype)
+    y_intra = scores @ vv
+    q_decay = torch.exp(idx.view(1, 1, 1, C, 1) * lg)
+    k_decay = torch.exp((C - 1 - idx).view(1, 1, 1, C, 1) * lg)
+    qd = _rnd(qf * q_decay, dtype)
+    kd = _rnd(kf * k_decay, dtype)
+    U = kd.transpose(-1, -2) @ vv  # [B,H,N,hk,hd]
+    gC = torch.exp(C * lg.view(1, H, 1, 1))
+    running = torch.zeros(B, H, hk, hd) if S0 is None else S0.float().clone()
+    y_inter = torch.empty_like(y_intra)
+    for n in range(N):
+        y_inter[:, :, n] = qd[:, :, n] @ _rnd(running, dtype)
+        running = running * gC + U[:, :, n]
+    y = (y_intra + y_inter).permute(0, 2, 3, 1, 4).reshape(B, L, H, hd)
+    return y, running
+
+
+# --------------------------------------------------------------------------------------
+# Per-token-per-head GroupNorm + sigmoid gate (model.py:274-295), row LayerNorm (model.py:382)
+# --------------------------------------------------------------------------------------
+def gnorm_gate(y, gate, gn_w, gn_b, H, eps=1e-5, pad_block=None):
+    """out = ((y-mu)/sqrt(var+eps) * w + b) * sigmoid(gate), statistics per (token, head).
+
+    ``y`` fp32 [B,L,H,hd]; ``gate`` [B,L,H*hd]; returns fp32 [B,L,H*hd].
+    ``pad_block`` (faithful mode) adds the (pad_block-hd)*mu^2/hd variance term of
+    the reference's unmasked centred lanes (model.py:290).
+    """
+    B, L, _, hd = y.shape
+    mean = y.mean(-1, keepdim=True)
+    yc = y - mean
+    var = (yc * yc).mean(-1, keepdim=True)
+    if pad_block is not None and pad_block > hd:
+        var = var + (pad_block - hd) * mean * mean / hd
+    w = gn_w.float().view(H, hd)
+    b = gn_b.float().view(H, hd)
+    ygn = yc / torch.sqrt(var + eps) * w + b
+    g = gate.float().view(B, L, H, hd)
+    out = ygn * (1.0 / (1.0 + torch.exp(-g)))
+    return out.reshape(B, L, H * hd)
+
+
+def rowln(x, w=None, b=None, eps=1e-5):
+    """LayerNorm over the last dim in fp32, output in x.dtype (model.py:382, nn.LayerNorm)."""
+    xf = x.float()
+    mean = xf.mean(-1, keepdim=True)
+    xc = xf - mean
+    var = (xc * xc).mean(-1, keepdim=True)
+    out = xc * torch.rsqrt(var + eps)
+    if w is not None:
+        out = out * w.float()
+    if b is not None:
+        out = out + b.float()
+    return out.to(x.dtype)
+
+
+# --------------------------------------------------------------------------------------
+# Faithful-mode address maps of the gate kernel launch (model.py:373-380, 288)
+# --------------------------------------------------------------------------------------
+def faithful_gate_index(B, L, dm, ds):
+    """Flat projs index the reference reads for gate[b,l,j]: its launch passes
+    stride_b=B*L and stride_l=4*dm for a view whose true strides are L*P and P
+    (model.py:373,377)."""
+    b = torch.arange(B).view(B, 1, 1)
+    l = torch.arange(L).view(1, L, 1)
+    j = torch.arange(dm).view(1, 1, dm)
+    return (3 * ds + 3 * dm) + b * (B * L) + l * (4 * dm) + j
+
+
+def faithful_yssm_index(B, L, ds):
+    """Flat y_ssm index read for token (b,l) channel d: batch stride passed as B*L
+    instead of L*ds (model.py:377)."""
+    b = torch.arange(B).view(B, 1, 1)
+    l = torch.arange(L).view(1, L, 1)
+    d = torch.arange(ds).view(1, 1, ds)
+    return b * (B * L) + l * ds + d
+
+
+def faithful_slot_position(L, C):
+    """Position within a head's flattened [N,C] y_slot read for token l: the gate kernel
+    computes (l//128, l%128) as (chunk, offset) whatever C is (model.py:288)."""
+    l = torch.arange(L)
+    return (l // 128) * C + (l % 128)
+
+
+# --------------------------------------------------------------------------------------
+# Block / model / LM forward (model.py:331-404, train_fineweb.py:86-94)
+# --------------------------------------------------------------------------------------
+def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_states=False):
+    """One HdcMamba9v3Block forward in eval mode (model.py:386-394 + 331-384).
+
+    ``p`` is the block's state_dict (tensors in the model dtype); ``x`` is [B,L,D].
+    """
+    dtype = x.dtype
+    dm, ds, H, C = cfg.d_model, cfg.d_state, cfg.num_heads, cfg.chunk_size
+    hd = cfg.head_dim
+    if semantics == "faithful" and C > 128:
+        raise ValueError("faithful semantics undefined for chunk_size > 128 (model.py:17,245-246)")
+    B, L_in, _ = x.shape
+    pad = (C - L_in % C) % C
+    if pad:
+        x = F.pad(x, (0, 0, pad, 0))
+    L = x.shape[1]
+    x_conv = norm_conv(x, p["norm.weight"], p["norm.bias"], p["conv1d.weight"].squeeze(1),
+                       p["conv1d.bias"], eps)
+    projs = F.linear(x_conv, p["in_proj.weight"].to(dtype), p["in_proj.bias"].to(dtype))
+    y_ssm, h_fin = ssm_chunked(projs, p["A_log"].to(dtype), ds, C, dtype, semantics)
+    gamma = p["gamma_buf"].to(dtype)
+    y_slot, s_fin = slot_chunked(projs, gamma, dm, ds, H, C, dtype, semantics)
+    gate = projs[..., 3 * ds + 3 * dm:]
+    if semantics == "faithful":
+        flat = projs.reshape(-1)
+        gate = flat[faithful_gate_index(B, L, dm, ds)]
+        pos = faithful_slot_position(L, C)
+        y_slot = _rnd(y_slot, dtype)[:, pos]
+        y_ssm_t = _rnd(y_ssm, dtype).reshape(-1)[faithful_yssm_index(B, L, ds)]
+        blk = max(64, 1 << (hd - 1).bit_length())
+        g = _rnd(gnorm_gate(y_slot, gate, p["group_norm.weight"], p["group_norm.bias"], H,
+                            pad_block=blk), torch.bfloat16)
+    else:
+        y_ssm_t = y_ssm
+        g = gnorm_gate(y_slot, gate, p["group_norm.weight"], p["group_norm.bias"], H)
+    combined = torch.cat([y_ssm_t.to(dtype), g.to(dtype)], -1)
+    c = F.layer_norm(combined.float(), (ds + dm,)).to(dtype)
+    res = F.linear(c, p["out_proj.weight"].to(dtype))
+    out = (x + res)[:, pad:, :]
+    if return_states:
+        return out, {"h": h_fin, "S": s_fin, "projs": projs, "combined": combined, "x_conv": x_conv}
+    return out
+
+
+def _sub(sd, prefix):
+    n = len(prefix)
+    return {k[n:]: v for k, v in sd.items() if k.startswith(prefix)}
+
+
+def model_forward(sd, x, cfg: BlockCfg, n_layers, semantics="intended", layers=None):
+    """HdcMamba9v3Model.forward (model.py:402-404): blocks then norm_final."""
+    for i in (range(n_layers) if layers is None else layers):
+        x = block_forward(_sub(sd, f"layers.{i}."), x, cfg, semantics)
+    return F.layer_norm(x, (cfg.d_model,), sd["norm_final.weight"], sd["norm_final.bias"], 1e-5)
+
+
+def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None):
+    """UniversalLM.forward, HdcMamba arm (train_fineweb.py:86-94): embedding, backbone,
+    norm_f, tied lm_head."""
+    x = F.embedding(ids, sd["embedding.weight"])
+    x = model_forward(_sub(sd, "backbone."), x, cfg, n_layers, semantics, layers)
+    x = F.layer_norm(x, (cfg.d_model,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)
+    return F.linear(x, sd["embedding.weight"])
+
+
+# --------------------------------------------------------------------------------------
+# Seeded parameter construction in the reference's RNG order (model.py:300-327,
+# train_fineweb.py:47-84).  Used by tests to build inputs independently of the product.
+# --------------------------------------------------------------------------------------
+def init_block_params(cfg: BlockCfg, generator_seed=None):
+    """State dict of a freshly constructed block, consuming the global RNG in the order
+    nn.Conv1d default init, normal_(std=.02), nn.Linear default init, torch.rand(ds),
+    xavier_uniform_ on q/k/v rows, nn.Linear default init of out_proj (model.py:306-327)."""
+    if generator_seed is not None:
+        torch.manual_seed(generator_seed)
+    dm, ds, H = cfg.d_model, cfg.d_state, cfg.num_heads
+    P = cfg.proj_width
+    conv = torch.nn.Conv1d(dm, dm, 4, groups=dm, padding=3, bias=True)
+    with torch.no_grad():
+        torch.nn.init.normal_(conv.weight, std=0.02)
+        conv.weight[:, 0, -1] += 1.0
+        conv.bias.fill_(0.0)
+    lin = torch.nn.Linear(dm, P, bias=True)
+    with torch.no_grad():
+        dt0 = torch.rand(ds) * (0.1 - 0.001) + 0.001
+        lin.bias[:ds] = torch.log(torch.exp(dt0) - 1.0)
+        torch.nn.init.xavier_uniform_(lin.weight[3 * ds:3 * ds + 3 * dm])
+        lin.bias[3 * ds + 3 * dm:].fill_(1.0)
+    A_log = torch.log(torch.linspace(0.99, 0.9999, ds))
+    decay_log = torch.log(torch.ones(H) * 0.05)
+    out = torch.nn.Linear(ds + dm, dm, bias=False)
+    return {
+        "norm.weight": torch.ones(dm), "norm.bias": torch.zeros(dm),
+        "conv1d.weight": conv.weight.detach().clone(), "conv1d.bias": conv.bias.detach().clone(),
+        "in_proj.weight": lin.weight.detach().clone(), "in_proj.bias": lin.bias.detach().clone(),
+        "A_log": A_log, "decay_log": decay_log,
+        "out_proj.weight": out.weight.detach().clone(),
+        "group_norm.weight": torch.ones(dm), "group_norm.bias": torch.zeros(dm),
+        "gamma_buf": torch.exp(-F.softplus(decay_log)),
+    }

@@ -1,0 +1,157 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (same seeded inputs).
+
+Tolerances: fp32 max-abs/rel 1e-4, bf16 2e-2 (assert_close atol=rtol).
+"""
+import pytest
+import torch
+
+import oracle
+from hdcmamba_amd import _ops
+from cfgs import assert_close, slot_inputs, ssm_inputs
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+# ----------------------------------------------------------------------------- norm_conv
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("D,L", [(256, 1), (256, 5), (768, 100), (1024, 257), (2048, 64)])
+def test_norm_conv(dev, dtype, D, L):
+    _say("norm_conv", dtype, D, L)
+    g = torch.Generator().manual_seed(D + L)
+    B = 2
+    x = (3 * torch.randn(B, L, D, generator=g) + 0.5).to(dtype)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=g)).to(dtype)
+    ln_b = (0.1 * torch.randn(D, generator=g)).to(dtype)
+    cw = (0.3 * torch.randn(D, 4, generator=g)).to(dtype)
+    cb = (0.1 * torch.randn(D, generator=g)).to(dtype)
+    out = _ops.norm_conv(x.to(dev), ln_w.to(dev), ln_b.to(dev), cw.to(dev), cb.to(dev), 1e-5)
+    ref = oracle.norm_conv(x, ln_w, ln_b, cw, cb, 1e-5)
+    assert_close(out, ref, dtype, "norm_conv")
+
+
+def test_norm_conv_batch_strided(dev):
+    """A batch-strided view (rows 3.. of a longer buffer) is read through its strides."""
+    g = torch.Generator().manual_seed(7)
+    D = 512
+    full = torch.randn(3, 40, D, generator=g)
+    x = full[:, 3:, :]
+    p = [torch.ones(D), torch.zeros(D) + 0.2, 0.3 * torch.randn(D, 4, generator=g), torch.zeros(D)]
+    out = _ops.norm_conv(full.to(dev)[:, 3:, :], *[t.to(dev) for t in p], 1e-5)
+    ref = oracle.norm_conv(x.contiguous(), *p, 1e-5)
+    assert_close(out, ref, torch.float32, "norm_conv strided")
+
+
+# ----------------------------------------------------------------------------- rowln
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("W", [320, 832, 1152, 2176])
+@pytest.mark.parametrize("affine", [False, True])
+def test_rowln(dev, dtype, W, affine):
+    _say("rowln", dtype, W, affine)
+    g = torch.Generator().manual_seed(W)
+    x = (5 * torch.randn(3, 37, W, generator=g) + 2).to(dtype)
+    w = (1 + 0.2 * torch.randn(W, generator=g)).to(dtype) if affine else None
+    b = (0.2 * torch.randn(W, generator=g)).to(dtype) if affine else None
+    xd = x.to(dev)
+    out = _ops.layer_norm(xd, w.to(dev) if affine else None, b.to(dev) if affine else None, 1e-5)
+    ref = oracle.rowln(x, w, b, 1e-5)
+    assert_close(out, ref, dtype, "rowln")
+    _ops.layer_norm(xd, w.to(dev) if affine else None, b.to(dev) if affine else None, 1e-5, out=xd)
+    assert_close(xd, ref, dtype, "rowln in place")
+
+
+# ----------------------------------------------------------------------------- ssm
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("ds,B,L", [(64, 1, 256), (128, 2, 200), (64, 3, 1000)])
+def test_ssm(dev, dtype, ds, B, L):
+    _say("ssm", dtype, ds, B, L)
+    projs, A_log = ssm_inputs(B, L, ds, dtype)
+    buf = torch.zeros(B, L, ds + 16, device=dev, dtype=dtype)
+    hf = torch.empty(B, ds, device=dev)
+    _ops.ssm(projs.to(dev), A_log.to(dev), ds, buf[..., :ds], h_final=hf)
+    y_ref, h_ref = oracle.ssm_sequential(projs, A_log, ds)
+    assert_close(buf[..., :ds], y_ref.to(dtype), dtype, "ssm y")
+    assert_close(hf, h_ref, dtype, "ssm h_final")
+    assert buf[..., ds:].abs().max().item() == 0.0
+
+
+def test_ssm_h0_continuation(dev):
+    """Running [0,L/2) then [L/2,L) with the carried state equals one run."""
+    ds, B, L = 64, 2, 512
+    projs, A_log = ssm_inputs(B, L, ds, torch.float32)
+    pd, ad = projs.to(dev), A_log.to(dev)
+    y = torch.empty(B, L, ds, device=dev)
+    _ops.ssm(pd, ad, ds, y)
+    y1 = torch.empty(B, L // 2, ds, device=dev)
+    y2 = torch.empty(B, L // 2, ds, device=dev)
+    h = torch.empty(B, ds, device=dev)
+    _ops.ssm(pd[:, :L // 2].contiguous(), ad, ds, y1, h_final=h)
+    _ops.ssm(pd[:, L // 2:].contiguous(), ad, ds, y2, h0=h)
+    assert_close(torch.cat([y1, y2], 1), y, torch.float32, "ssm split")
+
+
+# ----------------------------------------------------------------------------- slot + gate
+SLOT_CASES = [
+    # (dtype, B, L, dm, H, C)
+    (torch.float32, 1, 256, 256, 8, 64),     # hd 32
+    (torch.float32, 2, 192, 512, 8, 64),     # hd 64
+    (torch.float32, 1, 256, 768, 8, 64),     # hd 96
+    (torch.float32, 1, 256, 256, 4, 32),     # C = TC
+    (torch.float32, 1, 256, 256, 4, 16),     # C < TC: cross-chunk weights inside a tile
+    (torch.float32, 1, 512, 256, 4, 128),    # C > TC: carried within-chunk state
+    (torch.float32, 1, 512, 256, 4, 256),
+    (torch.bfloat16, 1, 256, 256, 8, 64),
+    (torch.bfloat16, 2, 512, 1024, 16, 64),  # hd 64
+    (torch.bfloat16, 1, 256, 768, 8, 64),    # hd 96
+    (torch.bfloat16, 1, 512, 512, 8, 32),
+    (torch.bfloat16, 1, 512, 512, 8, 256),
+]
+
+
+def _run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C, S0=None):
+    B, L, _ = projs.shape
+    pd = projs.to(dev)
+    hd = dm // H
+    out = torch.zeros(B, L, ds + dm, device=dev, dtype=projs.dtype)
+    ws = _ops.slot_workspace(pd, dm, H, C)
+    _ops.slot_state(pd, 3 * ds, gamma.to(dev), dm, H, C, ws, S0=S0)
+    sf = torch.empty(B, H, hd, hd, device=dev)
+    _ops.slot_gate(pd, 3 * ds, gamma.to(dev), gn_w.to(dev), gn_b.to(dev), 1e-5, ws, out, ds, dm, H, C,
+                   S_final=sf)
+    return out, sf
+
+
+@pytest.mark.parametrize("dtype,B,L,dm,H,C", SLOT_CASES)
+def test_slot_gate(dev, dtype, B, L, dm, H, C):
+    _say("slot_gate", dtype, B, L, dm, H, C)
+    ds = 64
+    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, dtype, seed=L + dm + C)
+    out, sf = _run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C)
+    y, S = oracle.slot_chunked(projs, gamma, dm, ds, H, C, dtype)
+    ref = oracle.gnorm_gate(y, projs[..., 3 * ds + 3 * dm:], gn_w, gn_b, H).to(dtype)
+    assert_close(out[..., ds:], ref, dtype, "slot+gate")
+    assert out[..., :ds].abs().max().item() == 0.0
+    assert_close(sf / S.abs().max(), S / S.abs().max(), dtype, "slot S_final")
+
+
+def test_slot_segments_env(dev, monkeypatch):
+    """Different segment lengths (state pre-pass on/off) give the same result."""
+    dm, ds, H, C, B, L = 256, 64, 4, 64, 1, 1024
+    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, torch.float32, seed=3)
+    outs = []
+    for st in ("1", "2", "16"):
+        monkeypatch.setenv("HDCM_SLOT_SEG_TILES", st)
+        outs.append(_run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C)[0])
+    for o in outs[1:]:
+        assert_close(o, outs[0], torch.float32, "segment invariance")
+
+
+def test_slot_unsupported_head_dim(dev):
+    projs, gamma, gn_w, gn_b = slot_inputs(1, 64, 240, 64, 5, torch.bfloat16)  # hd 48
+    with pytest.raises(_ops.HdcmError):
+        _run_slot(dev, projs, gamma, gn_w, gn_b, 240, 64, 5, 64)
