@@ -21,12 +21,17 @@ constexpr int kWave = 64;
 // ---------------------------------------------------------------- conversions
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
-}
+// Round-to-nearest-even through the gfx950 hardware conversion (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// Fast transcendentals: single v_exp_f32 / v_log_f32 / v_rcp_f32 instructions (about
+// 1 ulp on the instruction's own argument).
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float flog(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
@@ -151,7 +156,7 @@ __device__ __forceinline__ void frag_load4x2(Frag<float>& f, const float* p0, co
 // Build a fragment from 8 fp32 values, rounding to the operand type.
 __device__ __forceinline__ void frag_from_f32(Frag<bf16_t>& f, const float* x) {
 #pragma unroll
-  for (int s = 0; s < 8; ++s) f.v[s] = __builtin_bit_cast(__bf16, f2bf(x[s]));
+  for (int s = 0; s < 8; ++s) f.v[s] = (__bf16)x[s];
 }
 __device__ __forceinline__ void frag_from_f32(Frag<float>& f, const float* x) {
 #pragma unroll

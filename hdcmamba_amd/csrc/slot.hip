@@ -47,7 +47,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTargetWorkgroups = 2048;
+constexpr int kTargetWorkgroups = 1024;
+constexpr int kGateWavesPerEU = 3;  // register budget for 3 resident workgroups per CU
 constexpr int kMinSegTiles = 4;
 
 template <typename T>
@@ -58,27 +59,27 @@ struct TileOf {
 template <typename T, int HD, int TC>
 struct Lds {
   static constexpr int PADE = 16 / sizeof(T);
-  static constexpr int PR = HD + PADE;  // pitch of [TC][HD] row tiles and of [HD][HD] S^T
+  static constexpr int PR = HD + PADE;  // pitch of [TC][HD] row tiles and of the [HD][HD] S^T tile
   static constexpr int PT = TC + PADE;  // pitch of transposed [HD][TC] tiles
   static constexpr int tileR = TC * PR;
   static constexpr int tileT = HD * PT;
-  static constexpr int tileS = HD * PR;
-  static constexpr int oQ = 0;            // phi(q)            [TC][HD]
-  static constexpr int oQd = oQ + tileR;  // phi(q)*gamma^i    [TC][HD]
-  static constexpr int oK = oQd + tileR;  // phi(k)            [TC][HD]
-  static constexpr int oG = oK + tileR;   // gate (raw)        [TC][HD]
-  static constexpr int oKt = oG + tileR;  // (phi(k)*decay)^T  [HD][TC]
-  static constexpr int oVt = oKt + tileT; // v^T               [HD][TC]
-  static constexpr int oS0 = oVt + tileT; // S_eff^T buffers   [HD][HD] x2
-  static constexpr int oS1 = oS0 + tileS;
-  static constexpr int total = oS1 + tileS;
-  // state pre-pass uses only the two transposed tiles
+  static constexpr int oQ = 0;             // phi(q)            [TC][HD]
+  static constexpr int oK = oQ + tileR;    // phi(k)            [TC][HD]
+  static constexpr int oKt = oK + tileR;   // (phi(k)*decay)^T  [HD][TC]
+  static constexpr int oVt = oKt + tileT;  // v^T               [HD][TC]
+  static constexpr int oS = oVt + tileT;   // S_eff^T           [HD][HD]
+  static constexpr int total = oS + HD * PR;
+  // the state pre-pass uses only the two transposed tiles
   static constexpr int stKt = 0;
   static constexpr int stVt = tileT;
   static constexpr int stTotal = 2 * tileT;
 };
 
-__device__ __forceinline__ float phi_f(float z) { return z > 0.f ? z + 1.0f : expf(z); }
+// elu(z)+1 without a branch: z+1 for z>0, exp(z) otherwise.
+__device__ __forceinline__ float phi_f(float z) {
+  const float e = fexp(fminf(z, 0.f));
+  return z > 0.f ? z + 1.0f : e;
+}
 
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
@@ -92,6 +93,21 @@ __device__ __forceinline__ void store4<bf16_t>(bf16_t* p, const float* v) {
   u.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
   u.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
   *reinterpret_cast<uint2*>(p) = u;
+}
+
+// 4 consecutive elements from global memory as fp32.
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load4<float>(const float* p, float* v) {
+  const float4 u = *reinterpret_cast<const float4*>(p);
+  v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+}
+template <>
+__device__ __forceinline__ void load4<bf16_t>(const bf16_t* p, float* v) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  v[0] = __uint_as_float(u.x << 16); v[1] = __uint_as_float(u.x & 0xffff0000u);
+  v[2] = __uint_as_float(u.y << 16); v[3] = __uint_as_float(u.y & 0xffff0000u);
 }
 
 // Raw element e of a 16-byte group, as the storage type.
@@ -108,83 +124,106 @@ __device__ __forceinline__ bf16_t raw_elem<bf16_t>(const uint4& v, int e) {
   return (bf16_t)((e & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
-// Load the 16-byte groups of one tile owned by this thread.  Blocks are numbered
-// q=0, k=1, v=2, gate=3; the thread covers blocks [B0, B0+NB).  Each tile block has
-// TC*GPR groups, a multiple of kThreads, so the block of iteration `it` is uniform.
-template <typename T, int HD, int TC, int B0, int NB>
-__device__ __forceinline__ void load_tile(uint4 (&raw)[NB * HD / 32], const T* __restrict__ projs,
-                                          int64_t prs, int64_t rowbase, int colbase, int dm, int p,
-                                          int L, int tid) {
-  constexpr int E = Vec<T>::N;
-  constexpr int GPR = HD / E;
-  constexpr int NL = NB * HD / 32;
-  static_assert((TC * GPR) % kThreads == 0, "tile block must be a multiple of the workgroup");
-  static_assert(NL * kThreads == NB * TC * GPR, "load count");
+// Scale the 8 slots of a fragment by c, rounding to the operand type.
+__device__ __forceinline__ Frag<bf16_t> frag_scale(const Frag<bf16_t>& f, float c) {
+  Frag<bf16_t> o;
 #pragma unroll
-  for (int it = 0; it < NL; ++it) {
-    const int idx = tid + kThreads * it;
-    const int blk = B0 + (kThreads * it) / (TC * GPR);
-    const int rem = idx % (TC * GPR);
-    const int i = rem / GPR, cg = rem % GPR;
-    raw[it] = (p + i < L)
-                  ? ldg16(projs + (rowbase + p + i) * prs + colbase + blk * dm + cg * E)
-                  : make_uint4(0, 0, 0, 0);
-  }
+  for (int s = 0; s < 8; ++s) o.v[s] = (__bf16)((float)f.v[s] * c);
+  return o;
+}
+__device__ __forceinline__ Frag<float> frag_scale(const Frag<float>& f, float c) {
+  Frag<float> o;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) o.v[s] = f.v[s] * c;
+  return o;
 }
 
-// Write a loaded tile to LDS: phi/rounding/decay for q and k, transposes for k~ and v.
+// Tile loader.  The tile's q, k, v (blocks 0,1,2 relative to q_col) or only k, v
+// (B0=1, NB=2) are split into 16-byte groups; group idx = tid + 256*it covers block
+// B0 + (256*it)/(TC*GPR), row i, column group cg.  Offsets are relative to block B0.  TC*GPR is a multiple of 256, so the
+// block of each iteration is uniform and rows advance by whole tiles between calls.
+template <typename T, int HD, int TC, int B0, int NB>
+struct TileLoader {
+  static constexpr int E = Vec<T>::N;
+  static constexpr int GPR = HD / E;
+  static constexpr int NL = NB * TC * GPR / kThreads;
+  static_assert((TC * GPR) % kThreads == 0, "tile block must be a multiple of the workgroup");
+  int64_t off[NL];  // element offset of each group relative to the tile's first row
+  int row[NL];
+  __device__ __forceinline__ TileLoader(int64_t prs, int dm, int tid) {
+#pragma unroll
+    for (int it = 0; it < NL; ++it) {
+      const int idx = tid + kThreads * it;
+      const int blk = B0 + (kThreads * it) / (TC * GPR);
+      const int rem = idx % (TC * GPR);
+      row[it] = rem / GPR;
+      off[it] = (int64_t)row[it] * prs + (blk - B0) * dm + (rem % GPR) * E;
+    }
+  }
+  __device__ __forceinline__ void load(uint4 (&raw)[NL], const T* tile_base, int tlen) const {
+    if (tlen == TC) {
+#pragma unroll
+      for (int it = 0; it < NL; ++it) raw[it] = ldg16(tile_base + off[it]);
+    } else {
+#pragma unroll
+      for (int it = 0; it < NL; ++it)
+        raw[it] = row[it] < tlen ? ldg16(tile_base + off[it]) : make_uint4(0, 0, 0, 0);
+    }
+  }
+};
+
+// Write a loaded tile to LDS.  q: phi(q) row-major.  k: phi(k) row-major (unless
+// STATE_ONLY) and (phi(k)*gamma^(tlen-1-i))^T.  v: v^T.  Rows >= tlen are zero.
 template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY>
-__device__ __forceinline__ void stage_tile(const uint4 (&raw)[NB * HD / 32], T* sm, int tlen,
-                                           float lg, int tid) {
+__device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
+                                           int tlen, float lg2, int tid) {
   using LD = Lds<T, HD, TC>;
-  constexpr int E = Vec<T>::N;
-  constexpr int GPR = HD / E;
-  constexpr int NL = NB * HD / 32;
+  using TL = TileLoader<T, HD, TC, B0, NB>;
+  constexpr int E = TL::E, GPR = TL::GPR;
   T* sKt = sm + (STATE_ONLY ? LD::stKt : LD::oKt);
   T* sVt = sm + (STATE_ONLY ? LD::stVt : LD::oVt);
 #pragma unroll
-  for (int it = 0; it < NL; ++it) {
+  for (int it = 0; it < TL::NL; ++it) {
     const int idx = tid + kThreads * it;
     const int blk = B0 + (kThreads * it) / (TC * GPR);
     const int rem = idx % (TC * GPR);
     const int i = rem / GPR, cg = rem % GPR;
     const bool ok = i < tlen;
-    if (blk == 0) {  // q: phi(q) and phi(q)*gamma^i, row-major
-      float f[E], fd[E];
-      unpack16<T>(raw[it], f);
-      const float qd = expf((float)i * lg);
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        f[e] = ok ? rnd<T>(phi_f(f[e])) : 0.f;
-        fd[e] = f[e] * qd;
-      }
-      store16<T>(sm + LD::oQ + i * LD::PR + cg * E, f);
-      store16<T>(sm + LD::oQd + i * LD::PR + cg * E, fd);
-    } else if (blk == 1) {  // k: phi(k) row-major, (phi(k)*gamma^(tlen-1-i))^T
+    if (blk == 0) {
       float f[E];
       unpack16<T>(raw[it], f);
-      const float kd = ok ? expf((float)(tlen - 1 - i) * lg) : 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = ok ? rnd<T>(phi_f(f[e])) : 0.f;
-      if (!STATE_ONLY) store16<T>(sm + LD::oK + i * LD::PR + cg * E, f);
+      for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
+      store16<T>(sm + LD::oQ + i * LD::PR + cg * E, f);
+    } else if (blk == 1) {
+      float f[E];
+      unpack16<T>(raw[it], f);
+      const float kd = ok ? fexp2((float)(tlen - 1 - i) * lg2) : 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[e] = rnd<T>(phi_f(f[e]));
+      if (!STATE_ONLY) {
+        float g[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) g[e] = ok ? f[e] : 0.f;
+        store16<T>(sm + LD::oK + i * LD::PR + cg * E, g);
+      }
 #pragma unroll
       for (int e = 0; e < E; ++e) sKt[(cg * E + e) * LD::PT + i] = from_f<T>(f[e] * kd);
-    } else if (blk == 2) {  // v^T
+    } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) sVt[(cg * E + e) * LD::PT + i] = raw_elem<T>(raw[it], e);
-    } else {  // gate, copied as stored
-      *reinterpret_cast<uint4*>(sm + LD::oG + i * LD::PR + cg * E) = raw[it];
     }
   }
 }
 
 template <typename T, int HD, int TC, bool HAS_W>
-__global__ __launch_bounds__(kThreads) void slot_gate_kernel(
+__global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int dm, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
     int64_t ors, int out_col, float* __restrict__ S_final) {
   using LD = Lds<T, HD, TC>;
+  using TL = TileLoader<T, HD, TC, 0, 3>;
   static_assert(LD::total * sizeof(T) + 2 * HD * sizeof(float) <= 160 * 1024, "LDS budget");
   __shared__ __attribute__((aligned(16))) T sm[LD::total];
   __shared__ float sgw[HD], sgb[HD];
@@ -193,16 +232,18 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
   constexpr int NJS = TC / 32;  // K=32 steps across the tile rows
   constexpr int NIT = TC / 16;  // 16-row query tiles
   constexpr int OWN = (NVT + kWaves - 1) / kWaves;
-  constexpr int NL = HD / 8;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, kg = lane >> 4;
-  const int seg = blockIdx.x, h = blockIdx.y, b = blockIdx.z, H = gridDim.y;
-  const float lg = logf(to_f<T>(gamma[h]));
+  const int h = blockIdx.x, seg = blockIdx.y, b = blockIdx.z, H = gridDim.x;
+  const float lg2 = log2f(to_f<T>(gamma[h]));
+  const float ginv[4] = {1.0f, fexp2(-lg2), fexp2(-2.0f * lg2), fexp2(-3.0f * lg2)};
+  const bool one_chunk = cshift >= 31;  // C >= TC: every pair in a tile shares a chunk
   const int64_t rowbase = (int64_t)b * L;
   const int p_begin = seg * seg_tiles * TC;
   const int p_end = min(L, p_begin + seg_tiles * TC);
-  const int colbase = q_col + h * HD;
+  const T* colbase = projs + q_col + h * HD;
+  const T* gatebase = colbase + 3 * dm;
 
   if (tid < HD) {
     sgw[tid] = to_f<T>(gn_w[h * HD + tid]);
@@ -225,38 +266,72 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
       if constexpr (HAS_W) stW[ov][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   }
-  // S_eff for the first tile (segment starts on a chunk boundary): A.
-#pragma unroll
-  for (int ov = 0; ov < OWN; ++ov) {
-    const int vt = w + kWaves * ov;
-    if (vt < NVT) {
-#pragma unroll
-      for (int mt = 0; mt < NVT; ++mt) {
-        float v[4] = {stA[ov][mt][0], stA[ov][mt][1], stA[ov][mt][2], stA[ov][mt][3]};
-        store4<T>(sm + LD::oS0 + (vt * 16 + l16) * LD::PR + mt * 16 + kg * 4, v);
-      }
-    }
-  }
 
-  uint4 raw[NL];
-  load_tile<T, HD, TC, 0, 4>(raw, projs, prs, rowbase, colbase, dm, p_begin, L, tid);
-  int cur = 0;
+  const TL loader(prs, dm, tid);
+  uint4 raw[TL::NL];
+  loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
     __syncthreads();
-    stage_tile<T, HD, TC, 0, 4, false>(raw, sm, tlen, lg, tid);
-    if (p + TC < p_end) load_tile<T, HD, TC, 0, 4>(raw, projs, prs, rowbase, colbase, dm, p + TC, L, tid);
+    stage_tile<T, HD, TC, 0, 3, false>(raw, sm, tlen, lg2, tid);
+    // S_eff^T for this tile: gamma*W + gamma^(p-cs)*A (A alone when C divides TC).
+    {
+      float cA = 1.0f, cW = 0.0f;
+      if constexpr (HAS_W) {
+        cA = fexp2((float)(p % C) * lg2);
+        cW = fexp2(lg2);
+      }
+#pragma unroll
+      for (int ov = 0; ov < OWN; ++ov) {
+        const int vt = w + kWaves * ov;
+        if (vt >= NVT) continue;
+#pragma unroll
+        for (int mt = 0; mt < NVT; ++mt) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            v[r] = cA * stA[ov][mt][r];
+            if constexpr (HAS_W) v[r] += cW * stW[ov][mt][r];
+          }
+          store4<T>(sm + LD::oS + (vt * 16 + l16) * LD::PR + mt * 16 + kg * 4, v);
+        }
+      }
+    }
+    if (p + TC < p_end) loader.load(raw, colbase + (rowbase + p + TC) * prs, min(TC, L - p - TC));
     __syncthreads();
-    const T* sS = sm + (cur ? LD::oS1 : LD::oS0);
 
     // ---- outputs for query rows 16*w .. 16*w+15
     if (w < NIT) {
       const int it = w;
       const int iq = it * 16 + l16;
+      // gate values of this lane's output positions, loaded early
+      float gv[NVT][4];
+      if (iq < tlen) {
+        const T* grow = gatebase + (rowbase + p + iq) * prs + kg * 4;
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt) load4<T>(grow + vt * 16, gv[vt]);
+      }
       f32x4_t yacc[NVT];
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt) yacc[vt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      Frag<T> pf[NJS];
+      Frag<T> bq[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) frag_load8(bq[ks], sm + LD::oQ + iq * LD::PR + ks * 32 + kg * 8);
+      // y^T += S_eff^T (phi(q)*gamma^iq)^T
+      {
+        const float qd = fexp2((float)iq * lg2);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const Frag<T> bqd = frag_scale(bq[ks], qd);
+#pragma unroll
+          for (int vt = 0; vt < NVT; ++vt) {
+            Frag<T> a;
+            frag_load8(a, sm + LD::oS + (vt * 16 + l16) * LD::PR + ks * 32 + kg * 8);
+            yacc[vt] = mma(a, bqd, yacc[vt]);
+          }
+        }
+      }
+      // scores S^T[j][iq] for key tiles j <= it, decayed and masked, as P^T fragments
 #pragma unroll
       for (int t = 0; t < NJS; ++t) {
         if (2 * t > it) continue;
@@ -268,47 +343,36 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
           if (jt <= it) {
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
-              Frag<T> a, bq;
+              Frag<T> a;
               frag_load8(a, sm + LD::oK + (jt * 16 + l16) * LD::PR + ks * 32 + kg * 8);
-              frag_load8(bq, sm + LD::oQ + iq * LD::PR + ks * 32 + kg * 8);
-              s = mma(a, bq, s);
+              s = mma(a, bq[ks], s);
             }
           }
+          if (one_chunk) {
+            // gamma^(iq-j) = gamma^(iq-j0) * gamma^-r for the lane's 4 rows j = j0 + r
+            const int j0 = jt * 16 + kg * 4;
+            const float d0 = fexp2((float)(iq - j0) * lg2);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = jt * 16 + kg * 4 + r;
-            float v = 0.f;
-            if (jt <= it && j <= iq) {
+            for (int r = 0; r < 4; ++r)
+              pv[hh * 4 + r] = (jt <= it && j0 + r <= iq) ? s[r] * (d0 * ginv[r]) : 0.f;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int j = jt * 16 + kg * 4 + r;
               const int e = iq - j - (((iq >> cshift) != (j >> cshift)) ? 1 : 0);
-              v = s[r] * expf((float)e * lg);
+              pv[hh * 4 + r] = (jt <= it && j <= iq) ? s[r] * fexp2((float)e * lg2) : 0.f;
             }
-            pv[hh * 4 + r] = v;
           }
         }
-        frag_from_f32(pf[t], pv);
-      }
-      // y^T += V^T P^T (causal: only key tiles <= it)
-#pragma unroll
-      for (int t = 0; t < NJS; ++t) {
-        if (2 * t > it) continue;
+        Frag<T> pf;
+        frag_from_f32(pf, pv);
+        // y^T += V^T P^T over the 32 key rows of this step
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
           Frag<T> a;
           const T* base = sm + LD::oVt + (vt * 16 + l16) * LD::PT + 32 * t + kg * 4;
           frag_load4x2(a, base, base + 16);
-          yacc[vt] = mma(a, pf[t], yacc[vt]);
-        }
-      }
-      // y^T += S_eff^T (phi(q)*gamma^i)^T
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        Frag<T> bq;
-        frag_load8(bq, sm + LD::oQd + iq * LD::PR + ks * 32 + kg * 8);
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
-          Frag<T> a;
-          frag_load8(a, sS + (vt * 16 + l16) * LD::PR + ks * 32 + kg * 8);
-          yacc[vt] = mma(a, bq, yacc[vt]);
+          yacc[vt] = mma(a, pf, yacc[vt]);
         }
       }
       // GroupNorm over the head's HD values of row iq, then the sigmoid gate.
@@ -326,10 +390,9 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
           const float d = yacc[vt][r] - mean;
           sq += d * d;
         }
-      const float rinv = 1.0f / sqrtf(quad_group_sum(sq) * (1.0f / HD) + gn_eps);
+      const float rinv = rsqrtf(quad_group_sum(sq) * (1.0f / HD) + gn_eps);
       if (iq < tlen) {
-        T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD;
-        const T* grow = sm + LD::oG + iq * LD::PR;
+        T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + kg * 4;
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
           float o[4];
@@ -337,17 +400,16 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
           for (int r = 0; r < 4; ++r) {
             const int dv = vt * 16 + kg * 4 + r;
             const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
-            const float g = to_f<T>(grow[dv]);
-            o[r] = yn * (1.0f / (1.0f + expf(-g)));
+            o[r] = yn * frcp(1.0f + fexp(-gv[vt][r]));
           }
-          store4<T>(orow + vt * 16 + kg * 4, o);
+          store4<T>(orow + vt * 16, o);
         }
       }
     }
 
     // ---- state update: (W or A) <- gamma^tlen * (W or A) + K~^T V
     {
-      const float gt = expf((float)tlen * lg);
+      const float gt = fexp2((float)tlen * lg2);
 #pragma unroll
       for (int ov = 0; ov < OWN; ++ov) {
         const int vt = w + kWaves * ov;
@@ -373,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
       }
       if constexpr (HAS_W) {
         if (((p + tlen) % C) == 0) {
-          const float gC = expf((float)C * lg);
+          const float gC = fexp2((float)C * lg2);
 #pragma unroll
           for (int ov = 0; ov < OWN; ++ov)
 #pragma unroll
@@ -383,32 +445,6 @@ __global__ __launch_bounds__(kThreads) void slot_gate_kernel(
             }
         }
       }
-    }
-
-    // ---- S_eff^T for the next tile into the other buffer
-    if (p + TC < p_end) {
-      T* sSn = sm + (cur ? LD::oS0 : LD::oS1);
-      float cA = 1.0f, cW = 0.0f;
-      if constexpr (HAS_W) {
-        cA = expf((float)((p + TC) % C) * lg);
-        cW = expf(lg);
-      }
-#pragma unroll
-      for (int ov = 0; ov < OWN; ++ov) {
-        const int vt = w + kWaves * ov;
-        if (vt >= NVT) continue;
-#pragma unroll
-        for (int mt = 0; mt < NVT; ++mt) {
-          float v[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            v[r] = cA * stA[ov][mt][r];
-            if constexpr (HAS_W) v[r] += cW * stW[ov][mt][r];
-          }
-          store4<T>(sSn + (vt * 16 + l16) * LD::PR + mt * 16 + kg * 4, v);
-        }
-      }
-      cur ^= 1;
     }
   }
 
@@ -434,20 +470,20 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
                                                               int seg_tiles, int nseg,
                                                               float* __restrict__ U) {
   using LD = Lds<T, HD, TC>;
+  using TL = TileLoader<T, HD, TC, 1, 2>;
   __shared__ __attribute__((aligned(16))) T sm[LD::stTotal];
   constexpr int NVT = HD / 16;
   constexpr int NJS = TC / 32;
   constexpr int OWN = (NVT + kWaves - 1) / kWaves;
-  constexpr int NL = 2 * HD / 32;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, kg = lane >> 4;
-  const int seg = blockIdx.x, h = blockIdx.y, b = blockIdx.z, H = gridDim.y;
-  const float lg = logf(to_f<T>(gamma[h]));
+  const int h = blockIdx.x, seg = blockIdx.y, b = blockIdx.z, H = gridDim.x;
+  const float lg2 = log2f(to_f<T>(gamma[h]));
   const int64_t rowbase = (int64_t)b * L;
   const int p_begin = seg * seg_tiles * TC;
   const int p_end = min(L, p_begin + seg_tiles * TC);
-  const int colbase = q_col + h * HD;
+  const T* colbase = projs + q_col + dm + h * HD;  // k block; v follows at +dm
 
   f32x4_t st[OWN][NVT];
 #pragma unroll
@@ -455,15 +491,16 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
 #pragma unroll
     for (int mt = 0; mt < NVT; ++mt) st[ov][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint4 raw[NL];
-  load_tile<T, HD, TC, 1, 2>(raw, projs, prs, rowbase, colbase, dm, p_begin, L, tid);
+  const TL loader(prs, dm, tid);
+  uint4 raw[TL::NL];
+  loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
     __syncthreads();
-    stage_tile<T, HD, TC, 1, 2, true>(raw, sm, tlen, lg, tid);
-    if (p + TC < p_end) load_tile<T, HD, TC, 1, 2>(raw, projs, prs, rowbase, colbase, dm, p + TC, L, tid);
+    stage_tile<T, HD, TC, 1, 2, true>(raw, sm, tlen, lg2, tid);
+    if (p + TC < p_end) loader.load(raw, colbase + (rowbase + p + TC) * prs, min(TC, L - p - TC));
     __syncthreads();
-    const float gt = expf((float)tlen * lg);
+    const float gt = fexp2((float)tlen * lg2);
 #pragma unroll
     for (int ov = 0; ov < OWN; ++ov) {
       const int vt = w + kWaves * ov;
@@ -507,13 +544,26 @@ __global__ __launch_bounds__(kThreads) void slot_scan_kernel(const float* __rest
   const int e = blockIdx.x * kThreads + threadIdx.x;
   const int h = blockIdx.y, b = blockIdx.z, H = gridDim.y;
   if (e >= HD2) return;
-  const float gs = expf((float)seg_len * logf(to_f<T>(gamma[h])));
+  const float gs = fexp2((float)seg_len * log2f(to_f<T>(gamma[h])));
   const int64_t bh = (int64_t)b * H + h;
   float a = S0 ? S0[bh * HD2 + e] : 0.f;
-  const int64_t base = bh * nseg * HD2 + e;
-  for (int s = 0; s < nseg; ++s) {
-    Ain[base + (int64_t)s * HD2] = a;
-    if (s + 1 < nseg) a = a * gs + U[base + (int64_t)s * HD2];
+  const float* u = U + bh * nseg * HD2 + e;
+  float* o = Ain + bh * nseg * HD2 + e;
+  constexpr int kU = 8;
+  int s = 0;
+  for (; s + kU <= nseg; s += kU) {
+    float uu[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) uu[k] = (s + k + 1 < nseg) ? u[(int64_t)(s + k) * HD2] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+      o[(int64_t)(s + k) * HD2] = a;
+      a = a * gs + uu[k];
+    }
+  }
+  for (; s < nseg; ++s) {
+    o[(int64_t)s * HD2] = a;
+    if (s + 1 < nseg) a = a * gs + u[(int64_t)s * HD2];
   }
 }
 
@@ -581,7 +631,7 @@ int launch_state(const void* projs, int64_t prs, int64_t q_col, const void* gamm
   float* U = (float*)ws;
   float* Ain = U + (size_t)B * H * pl.nseg * HD * HD;
   if (pl.nseg > 1) {
-    hipLaunchKernelGGL((slot_state_kernel<T, HD, TC>), dim3(pl.nseg - 1, (unsigned)H, (unsigned)B),
+    hipLaunchKernelGGL((slot_state_kernel<T, HD, TC>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
                        dim3(kThreads), 0, s, (const T*)projs, prs, (int)q_col, (int)dm, (int)L,
                        (const T*)gamma, pl.seg_tiles, pl.nseg, U);
     const int st = hdcm_launch_status();
@@ -600,7 +650,8 @@ int launch_gate(const void* projs, int64_t prs, int64_t q_col, const void* gamma
                 int64_t H, int64_t C, const SlotPlan& pl, hipStream_t s) {
   constexpr int TC = TileOf<T>::value;
   const float* Ain = (const float*)ws + (size_t)B * H * pl.nseg * HD * HD;
-  dim3 grid(pl.nseg, (unsigned)H, (unsigned)B);
+  // heads vary fastest so the workgroups that run together read the same rows of projs
+  dim3 grid((unsigned)H, pl.nseg, (unsigned)B);
   if (pl.has_w)
     hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, true>), grid, dim3(kThreads), 0, s,
                        (const T*)projs, prs, (int)q_col, (int)dm, (int)L, (int)C, pl.cshift,

@@ -2,99 +2,170 @@
 //
 // Semantics (hdcmamba/model.py:175-233, intended form): per channel d and row t,
 //   dt = softplus(dt_raw) with threshold 20 (log(1+exp(x)) below it),
-//   ld = dt * A_d, A_d = -exp(A_log_d),  h_t = h_{t-1} * exp(ld) + dt * b * x,  y_t = h_t.
+//   a_t = exp(dt * A_d), A_d = -exp(A_log_d),  u_t = dt * b * x,
+//   h_t = a_t * h_{t-1} + u_t,  y_t = h_t.
 // All state is fp32; y is rounded once to the activation dtype.
 //
-// Work split: rows are cut into tiles of kTile.  Lanes map to channels (a wave reads 64
-// consecutive channels of a row, i.e. a contiguous 128/256-byte segment).
-//   1. ssm_tile_kernel   : per (tile, channel), scan from h=0 -> (sum ld, h_end).
-//   2. ssm_carry_kernel  : per channel, carry across tiles: Hin[n+1] = Hin[n]*exp(sum ld[n]) + h_end[n].
-//   3. ssm_out_kernel    : per (tile, channel), rescan from Hin[n] and store y.
-// The carry chain is one FMA per tile; its loads are independent of the chain and are
-// unrolled so they stay in flight.
+// The recurrence is the associative scan of pairs (a, u) under
+//   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2),
+// so a wave scans 64 consecutive rows of one channel with lanes = rows in six
+// shuffle steps instead of a 64-step serial loop.  Rows are cut into tiles of 64:
+//   1. ssm_tile_kernel<SUMMARY>: stage a tile's dt/x/b for 64 channels through LDS as
+//      (a, u) pairs, scan each channel, keep the tile total (A, H) [b][channel][tile].
+//   2. ssm_carry_kernel: per channel, scan the tile totals (lanes = groups of tiles) to
+//      get the state entering every tile, h_in[b][channel][tile], and h_final.
+//   3. ssm_tile_kernel<OUTPUT>: rescan each tile, y_t = U_t + A_t * h_in, staged back
+//      through LDS for 128-bit row stores.
 #include "hdcm_common.h"
 
 using namespace hdcm;
 
 namespace {
 
-constexpr int kTile = 64;
+constexpr int kTile = 64;      // rows per tile (= lanes of a wave)
+constexpr int kCh = 64;        // channels per workgroup
+constexpr int kThreads = 256;  // 4 waves, 16 channels each
+constexpr int kPitch = kCh + 1;
 
-__device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : logf(1.0f + expf(v)); }
+__device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : flog(1.0f + fexp(v)); }
 
-template <typename T>
-__global__ __launch_bounds__(kWave) void ssm_tile_kernel(const T* __restrict__ projs, int64_t prs,
-                                                         const T* __restrict__ A_log,
-                                                         float* __restrict__ sld_out,
-                                                         float* __restrict__ h_out, int L, int ds,
-                                                         int ntiles) {
-  const int d = blockIdx.y * kWave + threadIdx.x;
-  const int tile = blockIdx.x, b = blockIdx.z;
-  if (d >= ds) return;
-  const float A = -expf(to_f<T>(A_log[d]));
-  const int t0 = tile * kTile;
-  const int n = min(kTile, L - t0);
-  const T* p = projs + ((int64_t)b * L + t0) * prs + d;
-  float h = 0.f, sld = 0.f;
-#pragma unroll 8
-  for (int t = 0; t < n; ++t) {
-    const T* r = p + (int64_t)t * prs;
-    const float dt = softplus20(to_f<T>(r[0]));
-    const float xv = to_f<T>(r[ds]);
-    const float bv = to_f<T>(r[2 * ds]);
-    const float ld = dt * A;
-    sld += ld;
-    h = h * expf(ld) + dt * bv * xv;
+// Inclusive scan over the wave's lanes (row order) of (a, u) pairs.
+__device__ __forceinline__ void scan_pairs(float& a, float& u, int lane) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const float ap = __shfl_up(a, off, kWave);
+    const float up = __shfl_up(u, off, kWave);
+    if (lane >= off) {
+      u = a * up + u;
+      a = a * ap;
+    }
   }
-  const int64_t o = ((int64_t)b * ntiles + tile) * ds + d;
-  sld_out[o] = sld;
-  h_out[o] = h;
 }
 
-__global__ __launch_bounds__(kWave) void ssm_carry_kernel(const float* __restrict__ sld,
-                                                          const float* __restrict__ hend,
+template <typename T, bool OUTPUT>
+__global__ __launch_bounds__(kThreads) void ssm_tile_kernel(
+    const T* __restrict__ projs, int64_t prs, const T* __restrict__ A_log,
+    float* __restrict__ tot_a, float* __restrict__ tot_h, const float* __restrict__ hin,
+    T* __restrict__ y, int64_t yrs, float* __restrict__ h_final, int L, int ds, int ntiles) {
+  constexpr int E = Vec<T>::N;
+  constexpr int GPR = kCh / E;                       // 16-byte groups per row per block
+  constexpr int ITEMS = kTile * GPR / kThreads;      // (row, group) items per thread
+  __shared__ float sa[kTile * kPitch];
+  __shared__ float su[kTile * kPitch];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int tile = blockIdx.x, c0 = blockIdx.y * kCh, b = blockIdx.z;
+  const int t0 = tile * kTile;
+  const int tlen = min(kTile, L - t0);
+  const int nch = min(kCh, ds - c0);
+  const T* base = projs + ((int64_t)b * L + t0) * prs + c0;
+
+  // Stage (a, u) pairs.  Rows past the tile or channels past ds get the identity (1, 0).
+  uint4 rd[ITEMS], rx[ITEMS], rb[ITEMS];
+#pragma unroll
+  for (int k = 0; k < ITEMS; ++k) {
+    const int idx = tid + kThreads * k;
+    const int i = idx / GPR, cg = idx % GPR;
+    const bool ok = i < tlen && cg * E < nch;
+    const T* r = base + (int64_t)i * prs + cg * E;
+    rd[k] = ok ? ldg16(r) : make_uint4(0, 0, 0, 0);
+    rx[k] = ok ? ldg16(r + ds) : make_uint4(0, 0, 0, 0);
+    rb[k] = ok ? ldg16(r + 2 * ds) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int k = 0; k < ITEMS; ++k) {
+    const int idx = tid + kThreads * k;
+    const int i = idx / GPR, cg = idx % GPR;
+    const bool ok = i < tlen && cg * E < nch;
+    float d[E], xv[E], bv[E], al[E] = {};
+    unpack16<T>(rd[k], d);
+    unpack16<T>(rx[k], xv);
+    unpack16<T>(rb[k], bv);
+    if (ok) load16<T>(A_log + c0 + cg * E, al);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float dt = softplus20(d[e]);
+      const float A = -fexp(al[e]);
+      sa[i * kPitch + cg * E + e] = ok ? fexp(dt * A) : 1.0f;
+      su[i * kPitch + cg * E + e] = ok ? dt * bv[e] * xv[e] : 0.0f;
+    }
+  }
+  __syncthreads();
+
+  // Wave w scans channels w, w+4, ...; lane = row.
+  const int64_t tb = (int64_t)b * ds;
+  for (int c = w; c < nch; c += kThreads / kWave) {
+    float a = sa[lane * kPitch + c];
+    float u = su[lane * kPitch + c];
+    scan_pairs(a, u, lane);
+    const int64_t ci = (tb + c0 + c) * ntiles + tile;  // [b][channel][tile]
+    if constexpr (!OUTPUT) {
+      if (lane == kWave - 1) {
+        tot_a[ci] = a;
+        tot_h[ci] = u;
+      }
+    } else {
+      const float h = u + a * hin[ci];
+      su[lane * kPitch + c] = h;
+      if (h_final != nullptr && tile == ntiles - 1 && lane == tlen - 1) h_final[tb + c0 + c] = h;
+    }
+  }
+  if constexpr (OUTPUT) {
+    __syncthreads();
+    T* ybase = y + ((int64_t)b * L + t0) * yrs + c0;
+#pragma unroll
+    for (int k = 0; k < ITEMS; ++k) {
+      const int idx = tid + kThreads * k;
+      const int i = idx / GPR, cg = idx % GPR;
+      if (i < tlen && cg * E < nch) {
+        float v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = su[i * kPitch + cg * E + e];
+        store16<T>(ybase + (int64_t)i * yrs + cg * E, v);
+      }
+    }
+  }
+}
+
+// One wave per (channel, batch): lanes own consecutive groups of tiles.
+__global__ __launch_bounds__(kWave) void ssm_carry_kernel(const float* __restrict__ tot_a,
+                                                          const float* __restrict__ tot_h,
                                                           const float* __restrict__ h0,
                                                           float* __restrict__ hin,
                                                           float* __restrict__ h_final, int ds,
                                                           int ntiles) {
-  const int d = blockIdx.x * kWave + threadIdx.x;
-  const int b = blockIdx.y;
-  if (d >= ds) return;
-  float h = h0 ? h0[(int64_t)b * ds + d] : 0.f;
-  const int64_t base = (int64_t)b * ntiles * ds + d;
-#pragma unroll 8
-  for (int n = 0; n < ntiles; ++n) {
-    const int64_t o = base + (int64_t)n * ds;
-    hin[o] = h;
-    h = h * expf(sld[o]) + hend[o];
+  const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int64_t row = ((int64_t)b * ds + c) * ntiles;
+  const int per = (ntiles + kWave - 1) / kWave;
+  const int n0 = min(lane * per, ntiles), n1 = min(n0 + per, ntiles);
+  float A = 1.0f, Hs = 0.0f;
+  for (int n = n0; n < n1; ++n) {
+    const float a = tot_a[row + n];
+    Hs = a * Hs + tot_h[row + n];
+    A = A * a;
   }
-  if (h_final) h_final[(int64_t)b * ds + d] = h;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kWave) void ssm_out_kernel(const T* __restrict__ projs, int64_t prs,
-                                                        const T* __restrict__ A_log,
-                                                        const float* __restrict__ hin,
-                                                        T* __restrict__ y, int64_t yrs, int L,
-                                                        int ds, int ntiles) {
-  const int d = blockIdx.y * kWave + threadIdx.x;
-  const int tile = blockIdx.x, b = blockIdx.z;
-  if (d >= ds) return;
-  const float A = -expf(to_f<T>(A_log[d]));
-  const int t0 = tile * kTile;
-  const int n = min(kTile, L - t0);
-  const T* p = projs + ((int64_t)b * L + t0) * prs + d;
-  T* q = y + ((int64_t)b * L + t0) * yrs + d;
-  float h = hin[((int64_t)b * ntiles + tile) * ds + d];
-#pragma unroll 8
-  for (int t = 0; t < n; ++t) {
-    const T* r = p + (int64_t)t * prs;
-    const float dt = softplus20(to_f<T>(r[0]));
-    const float xv = to_f<T>(r[ds]);
-    const float bv = to_f<T>(r[2 * ds]);
-    h = h * expf(dt * A) + dt * bv * xv;
-    q[(int64_t)t * yrs] = from_f<T>(h);
+  // exclusive scan of the lane aggregates
+  float ia = A, ih = Hs;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const float ap = __shfl_up(ia, off, kWave);
+    const float hp = __shfl_up(ih, off, kWave);
+    if (lane >= off) {
+      ih = ia * hp + ih;
+      ia = ia * ap;
+    }
   }
+  float ea = __shfl_up(ia, 1, kWave), eh = __shfl_up(ih, 1, kWave);
+  if (lane == 0) {
+    ea = 1.0f;
+    eh = 0.0f;
+  }
+  const float init = h0 ? h0[(int64_t)b * ds + c] : 0.0f;
+  float h = ea * init + eh;
+  for (int n = n0; n < n1; ++n) {
+    hin[row + n] = h;
+    h = tot_a[row + n] * h + tot_h[row + n];
+  }
+  if (h_final != nullptr && n1 == ntiles && n0 < n1) h_final[(int64_t)b * ds + c] = h;
 }
 
 inline int64_t ssm_tiles(int64_t L) { return (L + kTile - 1) / kTile; }
@@ -105,21 +176,22 @@ int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, v
            hipStream_t s) {
   const int64_t nt = ssm_tiles(L);
   const int64_t n = B * nt * ds;
-  float* sld = (float*)ws;
-  float* hend = sld + n;
-  float* hin = hend + n;
-  const unsigned cg = (unsigned)((ds + kWave - 1) / kWave);
-  hipLaunchKernelGGL((ssm_tile_kernel<T>), dim3((unsigned)nt, cg, (unsigned)B), dim3(kWave), 0, s,
-                     (const T*)projs, prs, (const T*)A_log, sld, hend, (int)L, (int)ds, (int)nt);
+  float* ta = (float*)ws;
+  float* th = ta + n;
+  float* hin = th + n;
+  const dim3 grid((unsigned)nt, (unsigned)((ds + kCh - 1) / kCh), (unsigned)B);
+  hipLaunchKernelGGL((ssm_tile_kernel<T, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+                     (const T*)A_log, ta, th, (const float*)nullptr, (T*)nullptr, (int64_t)0,
+                     (float*)nullptr, (int)L, (int)ds, (int)nt);
   int st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL(ssm_carry_kernel, dim3(cg, (unsigned)B), dim3(kWave), 0, s, sld, hend, h0,
+  hipLaunchKernelGGL(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th, h0,
                      hin, h_final, (int)ds, (int)nt);
   st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL((ssm_out_kernel<T>), dim3((unsigned)nt, cg, (unsigned)B), dim3(kWave), 0, s,
-                     (const T*)projs, prs, (const T*)A_log, hin, (T*)y, yrs, (int)L, (int)ds,
-                     (int)nt);
+  hipLaunchKernelGGL((ssm_tile_kernel<T, true>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+                     (const T*)A_log, (float*)nullptr, (float*)nullptr, hin, (T*)y, yrs,
+                     (float*)nullptr, (int)L, (int)ds, (int)nt);
   return hdcm_launch_status();
 }
 
@@ -138,8 +210,10 @@ extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const vo
   HDCM_CHECK_ARG(projs && A_log && y, HDCM_EINVAL);
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && ds > 0, HDCM_EINVAL);
   HDCM_CHECK_ARG(proj_row_stride >= 3 * ds && y_row_stride >= ds, HDCM_EINVAL);
-  HDCM_CHECK_ARG(B <= 65535 && ssm_tiles(L) < ((int64_t)1 << 31) && ds <= 65535 * kWave,
-                 HDCM_EUNSUPPORTED);
+  const int E = 16 / hdcm_elt_size(dtype);
+  HDCM_CHECK_ARG(ds % E == 0 && proj_row_stride % E == 0 && y_row_stride % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(projs) && hdcm_aligned16(y) && hdcm_aligned16(A_log), HDCM_EALIGN);
+  HDCM_CHECK_ARG(B <= 65535 && ssm_tiles(L) < ((int64_t)1 << 31) && ds <= 65535, HDCM_EUNSUPPORTED);
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_ssm_workspace_bytes(B, L, ds), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 3u) == 0, HDCM_EALIGN);

@@ -46,7 +46,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
-    "BlockCfg", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
+    "BlockCfg", "kernel_rounding", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
     "slot_sequential", "slot_chunked", "gnorm_gate", "rowln", "block_forward",
     "model_forward", "lm_forward", "init_block_params",
 ]
@@ -68,8 +68,37 @@ class BlockCfg:
         return 3 * self.d_state + 4 * self.d_model
 
 
+# Rounding applied where the reference's Triton kernels convert fp32 values to bf16
+# (operand casts and stores).  "rne" is what a GPU does; "trunc" is what Triton's CPU
+# interpreter does (it drops the low 16 bits), used only to compare against vectors the
+# reference produced under the interpreter.  Rounding done by torch ops (F.linear,
+# F.layer_norm(...).to, the residual add) is always round-to-nearest-even.
+_KERNEL_ROUNDING = "rne"
+
+
+class kernel_rounding:
+    """Context manager selecting the kernel-side bf16 rounding mode ("rne" or "trunc")."""
+
+    def __init__(self, mode: str):
+        assert mode in ("rne", "trunc")
+        self.mode = mode
+
+    def __enter__(self):
+        global _KERNEL_ROUNDING
+        self.prev, _KERNEL_ROUNDING = _KERNEL_ROUNDING, self.mode
+        return self
+
+    def __exit__(self, *exc):
+        global _KERNEL_ROUNDING
+        _KERNEL_ROUNDING = self.prev
+
+
 def _rnd(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """Round fp32 values to ``dtype`` and back (no-op for fp32)."""
+    """Kernel-side rounding of fp32 values to ``dtype``, returned as fp32 (no-op for fp32)."""
+    if dtype == torch.float32:
+        return t.float()
+    if _KERNEL_ROUNDING == "trunc" and dtype == torch.bfloat16:
+        return (t.float().contiguous().view(torch.int32) & ~0xFFFF).view(torch.float32)
     return t.to(dtype).float()
 
 
@@ -107,7 +136,7 @@ def norm_conv(x, ln_w, ln_b, conv_w, conv_b, eps):
     up = torch.cat([b.expand(B, 3, D), u], dim=1)
     out = (up[:, 0:L] * cw[:, 0] + up[:, 1:L + 1] * cw[:, 1]
            + up[:, 2:L + 2] * cw[:, 2] + up[:, 3:L + 3] * cw[:, 3] + cb)
-    return out.to(dtype)
+    return _rnd(out, dtype).to(dtype)
 
 
 # --------------------------------------------------------------------------------------
@@ -360,7 +389,7 @@ def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_st
     else:
         y_ssm_t = y_ssm
         g = gnorm_gate(y_slot, gate, p["group_norm.weight"], p["group_norm.bias"], H)
-    combined = torch.cat([y_ssm_t.to(dtype), g.to(dtype)], -1)
+    combined = torch.cat([_rnd(y_ssm_t, dtype), _rnd(g, dtype)], -1).to(dtype)
     c = F.layer_norm(combined.float(), (ds + dm,)).to(dtype)
     res = F.linear(c, p["out_proj.weight"].to(dtype))
     out = (x + res)[:, pad:, :]

@@ -1,0 +1,126 @@
+"""The C ABI of libhdcmamba_hip.so on the CPU: the library loads, exports every entry
+point include/hdcm.h declares, and rejects bad arguments before touching the GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from hdcmamba_amd import _ops
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "hdcm.h"
+OK, EINVAL, EALIGN, EUNSUPPORTED, ELAUNCH, EWORKSPACE = 0, -1, -2, -3, -4, -5
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hdcm_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _ops.lib()
+    names = declared()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(_ops._PROTOS) == names, "ctypes prototypes out of step with include/hdcm.h"
+
+
+def test_abi_version_and_strerror():
+    lib = _ops.lib()
+    assert lib.hdcm_abi_version() == _ops.ABI_VERSION
+    for code in (OK, EINVAL, EALIGN, EUNSUPPORTED, ELAUNCH, EWORKSPACE):
+        assert lib.hdcm_strerror(code)
+    assert b"unknown" in lib.hdcm_strerror(123)
+
+
+def test_workspace_sizes():
+    lib = _ops.lib()
+    assert lib.hdcm_ssm_workspace_bytes(1, 32768, 128) == 3 * 512 * 128 * 4
+    assert lib.hdcm_ssm_workspace_bytes(0, 10, 4) == 0
+    n = lib.hdcm_slot_workspace_bytes(1, 32768, 1024, 16, 64, _ops.HDCM_BF16)
+    assert n > 0 and n % (2 * 16 * 64 * 64 * 4) == 0
+    assert lib.hdcm_slot_workspace_bytes(1, 64, 240, 5, 64, _ops.HDCM_BF16) == 0  # head dim 48
+    assert lib.hdcm_slot_workspace_bytes(1, 96, 256, 4, 48, _ops.HDCM_BF16) == 0  # chunk 48
+
+
+P16 = ctypes.c_void_p(16 * 1024)       # aligned non-null stand-ins: never dereferenced,
+P17 = ctypes.c_void_p(16 * 1024 + 2)   # every call below fails validation first
+
+
+def test_norm_conv_validation():
+    f = _ops.lib().hdcm_norm_conv_fwd
+    args = [P16, 256 * 64, 64, P16, P16, P16, P16, P16, 256 * 64, 64, 1, 256, 64, 1e-5, 1, None]
+    bad_null = list(args); bad_null[0] = None
+    assert f(*bad_null) == EINVAL
+    bad_align = list(args); bad_align[0] = P17
+    assert f(*bad_align) == EALIGN
+    bad_d = list(args); bad_d[12] = 63
+    assert f(*bad_d) == EALIGN
+    bad_dtype = list(args); bad_dtype[14] = 7
+    assert f(*bad_dtype) == EUNSUPPORTED
+    empty = list(args); empty[11] = 0
+    assert f(*empty) == OK  # nothing to do, no launch
+
+
+def test_ssm_validation():
+    f = _ops.lib().hdcm_ssm_fwd
+    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, P16, 1 << 20, 1, 256, 64, 1, None]
+    a = list(base); a[7] = None
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[8] = 16
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[1] = 100
+    assert f(*a) == EINVAL
+    a = list(base); a[0] = P17
+    assert f(*a) == EALIGN
+
+
+def test_slot_validation():
+    lib = _ops.lib()
+    st = lib.hdcm_slot_state_fwd
+    base = [P16, 3 * 64 + 4 * 256, 3 * 64, P16, None, P16, 1 << 24, 1, 256, 256, 4, 64, 1, None]
+    a = list(base); a[10] = 5  # 256 % 5 != 0
+    assert st(*a) == EINVAL
+    a = list(base); a[8] = 250  # L not a multiple of C
+    assert st(*a) == EINVAL
+    a = list(base); a[11] = 48; a[8] = 96  # chunk 48 neither divides nor is a multiple of 64
+    assert st(*a) == EUNSUPPORTED
+    a = list(base); a[5] = None
+    assert st(*a) == EWORKSPACE
+    a = list(base); a[1] = 256  # row too short for q,k,v,gate
+    assert st(*a) == EINVAL
+    g = lib.hdcm_slot_gate_fwd
+    gb = [P16, 3 * 64 + 4 * 256, 3 * 64, P16, P16, P16, 1e-5, P16, 1 << 24, P16, 64 + 256, 64, None,
+          1, 256, 256, 4, 64, 1, None]
+    a = list(gb); a[11] = 62  # output runs of 4 must stay aligned
+    assert g(*a) == EALIGN
+    a = list(gb); a[10] = 200  # output row too short
+    assert g(*a) == EINVAL
+
+
+def test_rowln_validation():
+    f = _ops.lib().hdcm_rowln_fwd
+    base = [P16, 1152, P16, 1152, None, None, 10, 1152, 1e-5, 1, None]
+    a = list(base); a[4] = P16  # w without b
+    assert f(*a) == EINVAL
+    a = list(base); a[7] = 1150
+    assert f(*a) == EALIGN
+    a = list(base); a[7] = 8 * 13 * 64  # wider than the kernel's register tiling
+    a[1] = a[3] = a[7]
+    assert f(*a) == EUNSUPPORTED
+
+
+def test_cpu_tensors_raise():
+    """No CPU fallback: the product path refuses host tensors."""
+    from hdcmamba_amd import HdcMamba9v3Block, HdcMamba9v3Model
+
+    blk = HdcMamba9v3Block(64, 16, 2, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        blk(torch.randn(1, 64, 64))
+    with pytest.raises(RuntimeError, match="GPU"):
+        HdcMamba9v3Model(64, 1, 16, 32, 2)(torch.randn(1, 64, 64))
+    with pytest.raises(RuntimeError, match="GPU"):
+        _ops.norm_conv(torch.randn(1, 4, 64), torch.ones(64), torch.zeros(64), torch.zeros(64, 4),
+                       torch.zeros(64), 1e-5)
