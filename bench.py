@@ -61,7 +61,7 @@ def cpu_baseline(model, ids_gpu, cfg, budget_s):
     threads = min(threads, int(os.environ.get("HDCM_CPU_THREADS", "16")))
     torch.set_num_threads(threads)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
-    L = min(cfg["L"], 4096)
+    L = cfg["L"]
     ids = ids_gpu[:1, :L].cpu()
     bcfg = oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"])
     n_layers = cfg["n_layers"]

@@ -85,8 +85,9 @@ class HdcMamba9v3Block(nn.Module):
         self.group_norm = nn.GroupNorm(num_heads, d_model)
         self.register_buffer("gamma_buf", torch.exp(-F.softplus(self.decay_log)))
 
-    def _inner_forward(self, x):
-        """Block body on a chunk-aligned [B,L,dm] input; returns out_proj(LN(combined)) + x."""
+    def _mixer(self, x):
+        """LN+conv, in_proj, SSM and slot+gate into one `combined` row buffer, then its
+        LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm]."""
         B, L, dm = x.shape
         ds, H, C = self.d_state, self.num_heads, self.chunk_size
         dtype = x.dtype
@@ -101,9 +102,22 @@ class HdcMamba9v3Block(nn.Module):
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
                        combined, ds, dm, H, C)
         _ops.layer_norm(combined, eps=1e-5, out=combined)
-        out = torch.addmm(x.reshape(B * L, dm), combined.view(B * L, ds + dm),
-                          self.out_proj.weight.to(dtype).t())
+        return combined.view(B * L, ds + dm)
+
+    def _inner_forward(self, x):
+        """Block body on a chunk-aligned [B,L,dm] input; returns x + out_proj(LN(combined))."""
+        B, L, dm = x.shape
+        c = self._mixer(x)
+        out = torch.addmm(x.reshape(B * L, dm), c, self.out_proj.weight.to(x.dtype).t())
         return out.view(B, L, dm)
+
+    def _residual_step_(self, r):
+        """In-place variant for a model-owned residual stream r [B,L,dm] (chunk-aligned):
+        r += out_proj(LN(combined)), with the GEMM accumulating straight into r."""
+        B, L, dm = r.shape
+        c = self._mixer(r)
+        r.view(B * L, dm).addmm_(c, self.out_proj.weight.to(r.dtype).t())
+        return r
 
     def forward(self, x):
         _ops._on_gpu(x)
@@ -133,7 +147,24 @@ class HdcMamba9v3Model(nn.Module):
         self.norm_final = nn.LayerNorm(d_model)
 
     def forward(self, x):
-        for layer in self.layers:
-            x, _ = layer(x)
+        _ops._on_gpu(x)
+        chunks = {layer.chunk_size for layer in self.layers}
+        if torch.is_grad_enabled() or len(chunks) != 1 or self.training:
+            for layer in self.layers:
+                x, _ = layer(x)
+        else:
+            # Inference: one residual stream updated in place by every block.  Each block
+            # of the reference left-pads its own input with zero rows (model.py:388-389), so
+            # the pad rows are zeroed again before every block.
+            (C,) = chunks
+            B, L, dm = x.shape
+            pad = (C - L % C) % C
+            r = torch.empty(B, L + pad, dm, device=x.device, dtype=x.dtype)
+            r[:, pad:].copy_(x)
+            for layer in self.layers:
+                if pad:
+                    r[:, :pad].zero_()
+                layer._residual_step_(r)
+            x = r[:, pad:]
         return _ops.layer_norm(x.contiguous(), self.norm_final.weight, self.norm_final.bias,
                                self.norm_final.eps)

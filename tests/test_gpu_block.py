@@ -68,3 +68,23 @@ def test_cpu_tensor_raises():
     blk = HdcMamba9v3Block(64, 16, 2, 64)
     with pytest.raises(RuntimeError, match="GPU"):
         blk(torch.randn(1, 64, 64))
+
+
+@pytest.mark.parametrize("L", [192, 100])
+def test_model_inplace_stream(dev, L):
+    """HdcMamba9v3Model under no_grad updates one residual stream in place; with a length
+    that needs padding the pad rows must be re-zeroed before every block."""
+    print("model inplace", L, flush=True)
+    from hdcmamba_amd import HdcMamba9v3Model
+    from cfgs import reinit_block_
+
+    torch.manual_seed(3)
+    m = HdcMamba9v3Model(256, 3, 64, 32, num_heads=4, chunk_size=64)
+    for i, blk in enumerate(m.layers):
+        reinit_block_(blk, seed=10 + i)
+    m = m.eval()
+    x = torch.randn(2, L, 256, generator=torch.Generator().manual_seed(L))
+    ref = oracle.model_forward(_sd(m), x, oracle.BlockCfg(256, 64, 4, 64), 3)
+    with torch.no_grad():
+        y = m.to(dev)(x.to(dev))
+    assert_close(y, ref, torch.float32, f"model L={L}")
