@@ -47,8 +47,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTargetWorkgroups = 1024;
-constexpr int kGateWavesPerEU = 3;  // register budget for 3 resident workgroups per CU
+constexpr int kTargetWorkgroups = 512;
+constexpr int kGateWavesPerEU = 2;  // register budget for the gate kernel (waves per SIMD)
 constexpr int kMinSegTiles = 4;
 
 template <typename T>
@@ -56,30 +56,59 @@ struct TileOf {
   static constexpr int value = sizeof(T) == 2 ? 64 : 32;
 };
 
+// LDS tiles.  Row tiles [TC][HD] hold phi(q) and phi(k); transposed tiles [HD][TC] hold
+// (phi(k)*decay)^T and v^T; the S tile [HD][HD] holds S_eff^T.  Where a row spans a
+// multiple of 8 16-byte chunks the chunks are XOR-swizzled, chunk ^ ((row + row/8) % 8),
+// instead of padded: the transposed 2-byte stores of a wave (8 rows x 8 column groups)
+// then hit 32 distinct dwords, and 16-byte fragment reads of 16 consecutive rows hit
+// distinct bank groups.  Other row lengths are padded by one chunk.
 template <typename T, int HD, int TC>
 struct Lds {
-  static constexpr int PADE = 16 / sizeof(T);
-  static constexpr int PR = HD + PADE;  // pitch of [TC][HD] row tiles and of the [HD][HD] S^T tile
-  static constexpr int PT = TC + PADE;  // pitch of transposed [HD][TC] tiles
+  static constexpr int E = 16 / sizeof(T);  // elements per 16-byte chunk
+  static constexpr bool SW_R = (HD / E) % 8 == 0;
+  static constexpr bool SW_T = (TC / E) % 8 == 0;
+  static constexpr int PR = SW_R ? HD : HD + E;  // pitch of row tiles and of the S tile
+  static constexpr int PT = SW_T ? TC : TC + E;  // pitch of transposed tiles
   static constexpr int tileR = TC * PR;
   static constexpr int tileT = HD * PT;
-  static constexpr int oQ = 0;             // phi(q)            [TC][HD]
-  static constexpr int oK = oQ + tileR;    // phi(k)            [TC][HD]
-  static constexpr int oKt = oK + tileR;   // (phi(k)*decay)^T  [HD][TC]
-  static constexpr int oVt = oKt + tileT;  // v^T               [HD][TC]
-  static constexpr int oS = oVt + tileT;   // S_eff^T           [HD][HD]
+  static constexpr int oQ = 0;
+  static constexpr int oK = oQ + tileR;
+  static constexpr int oKt = oK + tileR;
+  static constexpr int oVt = oKt + tileT;
+  static constexpr int oS = oVt + tileT;
   static constexpr int total = oS + HD * PR;
   // the state pre-pass uses only the two transposed tiles
   static constexpr int stKt = 0;
   static constexpr int stVt = tileT;
   static constexpr int stTotal = 2 * tileT;
+
+  __device__ static __forceinline__ int swz(int row, int col) {
+    return (((col / E) ^ ((row + (row >> 3)) & 7)) * E) + (col % E);
+  }
+  // element offset of (row, col) in a row tile / the S tile, and in a transposed tile
+  __device__ static __forceinline__ int r_at(int row, int col) {
+    return row * PR + (SW_R ? swz(row, col) : col);
+  }
+  __device__ static __forceinline__ int t_at(int row, int col) {
+    return row * PT + (SW_T ? swz(row, col) : col);
+  }
 };
 
-// elu(z)+1 without a branch: z+1 for z>0, exp(z) otherwise.
-__device__ __forceinline__ float phi_f(float z) {
-  const float e = fexp(fminf(z, 0.f));
-  return z > 0.f ? z + 1.0f : e;
+// Fragment of 8 consecutive columns col..col+7 of `row` (col a multiple of 8).
+template <typename T, int HD, int TC, bool TRANSPOSED>
+__device__ __forceinline__ void lds_frag8(Frag<T>& f, const T* tile, int row, int col) {
+  using LD = Lds<T, HD, TC>;
+  auto at = [](int r, int c) { return TRANSPOSED ? LD::t_at(r, c) : LD::r_at(r, c); };
+  if constexpr (sizeof(T) == 2) {
+    frag_load8(f, tile + at(row, col));
+  } else {
+    frag_load4x2(f, tile + at(row, col), tile + at(row, col + 4));
+  }
 }
+
+// elu(z)+1 without a branch or select: exp(min(z,0)) + max(z,0) is exp(z) for z<=0 and
+// 1+z for z>0.
+__device__ __forceinline__ float phi_f(float z) { return fexp(fminf(z, 0.f)) + fmaxf(z, 0.f); }
 
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
@@ -174,9 +203,9 @@ struct TileLoader {
 
 // Write a loaded tile to LDS.  q: phi(q) row-major.  k: phi(k) row-major (unless
 // STATE_ONLY) and (phi(k)*gamma^(tlen-1-i))^T.  v: v^T.  Rows >= tlen are zero.
-template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY>
-__device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
-                                           int tlen, float lg2, int tid) {
+template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY, bool FULL>
+__device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
+                                                int tlen, float lg2, int tid) {
   using LD = Lds<T, HD, TC>;
   using TL = TileLoader<T, HD, TC, B0, NB>;
   constexpr int E = TL::E, GPR = TL::GPR;
@@ -188,13 +217,13 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
     const int blk = B0 + (kThreads * it) / (TC * GPR);
     const int rem = idx % (TC * GPR);
     const int i = rem / GPR, cg = rem % GPR;
-    const bool ok = i < tlen;
+    const bool ok = FULL || i < tlen;
     if (blk == 0) {
       float f[E];
       unpack16<T>(raw[it], f);
 #pragma unroll
       for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
-      store16<T>(sm + LD::oQ + i * LD::PR + cg * E, f);
+      store16<T>(sm + LD::oQ + LD::r_at(i, cg * E), f);
     } else if (blk == 1) {
       float f[E];
       unpack16<T>(raw[it], f);
@@ -205,19 +234,28 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
         float g[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) g[e] = ok ? f[e] : 0.f;
-        store16<T>(sm + LD::oK + i * LD::PR + cg * E, g);
+        store16<T>(sm + LD::oK + LD::r_at(i, cg * E), g);
       }
 #pragma unroll
-      for (int e = 0; e < E; ++e) sKt[(cg * E + e) * LD::PT + i] = from_f<T>(f[e] * kd);
+      for (int e = 0; e < E; ++e) sKt[LD::t_at(cg * E + e, i)] = from_f<T>(f[e] * kd);
     } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) sVt[(cg * E + e) * LD::PT + i] = raw_elem<T>(raw[it], e);
+      for (int e = 0; e < E; ++e) sVt[LD::t_at(cg * E + e, i)] = raw_elem<T>(raw[it], e);
     }
   }
 }
 
+template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY>
+__device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
+                                           int tlen, float lg2, int tid) {
+  if (tlen == TC)
+    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, true>(raw, sm, tlen, lg2, tid);
+  else
+    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, false>(raw, sm, tlen, lg2, tid);
+}
+
 template <typename T, int HD, int TC, bool HAS_W>
-__global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
+__global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int dm, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
@@ -293,7 +331,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
             v[r] = cA * stA[ov][mt][r];
             if constexpr (HAS_W) v[r] += cW * stW[ov][mt][r];
           }
-          store4<T>(sm + LD::oS + (vt * 16 + l16) * LD::PR + mt * 16 + kg * 4, v);
+          store4<T>(sm + LD::oS + LD::r_at(vt * 16 + l16, mt * 16 + kg * 4), v);
         }
       }
     }
@@ -316,7 +354,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
       for (int vt = 0; vt < NVT; ++vt) yacc[vt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       Frag<T> bq[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) frag_load8(bq[ks], sm + LD::oQ + iq * LD::PR + ks * 32 + kg * 8);
+      for (int ks = 0; ks < NKS; ++ks) lds_frag8<T, HD, TC, false>(bq[ks], sm + LD::oQ, iq, ks * 32 + kg * 8);
       // y^T += S_eff^T (phi(q)*gamma^iq)^T
       {
         const float qd = fexp2((float)iq * lg2);
@@ -326,7 +364,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
 #pragma unroll
           for (int vt = 0; vt < NVT; ++vt) {
             Frag<T> a;
-            frag_load8(a, sm + LD::oS + (vt * 16 + l16) * LD::PR + ks * 32 + kg * 8);
+            lds_frag8<T, HD, TC, false>(a, sm + LD::oS, vt * 16 + l16, ks * 32 + kg * 8);
             yacc[vt] = mma(a, bqd, yacc[vt]);
           }
         }
@@ -344,7 +382,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
               Frag<T> a;
-              frag_load8(a, sm + LD::oK + (jt * 16 + l16) * LD::PR + ks * 32 + kg * 8);
+              lds_frag8<T, HD, TC, false>(a, sm + LD::oK, jt * 16 + l16, ks * 32 + kg * 8);
               s = mma(a, bq[ks], s);
             }
           }
@@ -370,8 +408,9 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
           Frag<T> a;
-          const T* base = sm + LD::oVt + (vt * 16 + l16) * LD::PT + 32 * t + kg * 4;
-          frag_load4x2(a, base, base + 16);
+          const int row = vt * 16 + l16;
+          frag_load4x2(a, sm + LD::oVt + LD::t_at(row, 32 * t + kg * 4),
+                       sm + LD::oVt + LD::t_at(row, 32 * t + 16 + kg * 4));
           yacc[vt] = mma(a, pf, yacc[vt]);
         }
       }
@@ -417,7 +456,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
         Frag<T> bv[NJS];
 #pragma unroll
         for (int ks = 0; ks < NJS; ++ks)
-          frag_load8(bv[ks], sm + LD::oVt + (vt * 16 + l16) * LD::PT + ks * 32 + kg * 8);
+          lds_frag8<T, HD, TC, true>(bv[ks], sm + LD::oVt, vt * 16 + l16, ks * 32 + kg * 8);
 #pragma unroll
         for (int mt = 0; mt < NVT; ++mt) {
           f32x4_t acc;
@@ -426,7 +465,7 @@ __global__ __launch_bounds__(kThreads, kGateWavesPerEU) void slot_gate_kernel(
 #pragma unroll
           for (int ks = 0; ks < NJS; ++ks) {
             Frag<T> a;
-            frag_load8(a, sm + LD::oKt + (mt * 16 + l16) * LD::PT + ks * 32 + kg * 8);
+            lds_frag8<T, HD, TC, true>(a, sm + LD::oKt, mt * 16 + l16, ks * 32 + kg * 8);
             acc = mma(a, bv[ks], acc);
           }
           if constexpr (HAS_W) stW[ov][mt] = acc;
@@ -508,14 +547,14 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
       Frag<T> bv[NJS];
 #pragma unroll
       for (int ks = 0; ks < NJS; ++ks)
-        frag_load8(bv[ks], sm + LD::stVt + (vt * 16 + l16) * LD::PT + ks * 32 + kg * 8);
+        lds_frag8<T, HD, TC, true>(bv[ks], sm + LD::stVt, vt * 16 + l16, ks * 32 + kg * 8);
 #pragma unroll
       for (int mt = 0; mt < NVT; ++mt) {
         f32x4_t acc = st[ov][mt] * gt;
 #pragma unroll
         for (int ks = 0; ks < NJS; ++ks) {
           Frag<T> a;
-          frag_load8(a, sm + LD::stKt + (mt * 16 + l16) * LD::PT + ks * 32 + kg * 8);
+          lds_frag8<T, HD, TC, true>(a, sm + LD::stKt, mt * 16 + l16, ks * 32 + kg * 8);
           acc = mma(a, bv[ks], acc);
         }
         st[ov][mt] = acc;
