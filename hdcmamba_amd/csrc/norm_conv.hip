@@ -10,6 +10,8 @@
 // the taps:  out = sum_k (w*c_k) * xhat[t-3+k] + (b*sum_k c_k + c_b), xhat = (x-mu)*rstd,
 // which makes the t<0 halo exactly xhat = 0.  Raw rows are prefetched PF rows ahead so
 // several 128-bit loads per lane are in flight while the current row is reduced.
+#include <stdlib.h>
+
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -17,8 +19,7 @@ using namespace hdcm;
 namespace {
 
 constexpr int kWavesPerBlock = 4;
-constexpr int kRows = 16;  // rows per wave
-constexpr int kPF = 3;     // prefetch distance (rows)
+constexpr int kPF = 3;  // prefetch distance (rows)
 
 template <typename T, int NG>
 __device__ __forceinline__ void load_row(uint4 (&raw)[NG], const T* row, int lane, int G) {
@@ -61,7 +62,7 @@ __device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&xh)[NG][V
     for (int e = 0; e < E; ++e) xh[i][e] *= rstd;
 }
 
-template <typename T, int NG>
+template <typename T, int NG, int kRows>
 __global__ __launch_bounds__(kWavesPerBlock* kWave) void norm_conv_kernel(
     const T* __restrict__ x, int64_t x_bs, int64_t x_rs, const T* __restrict__ ln_w,
     const T* __restrict__ ln_b, const T* __restrict__ conv_w, const T* __restrict__ conv_b,
@@ -166,15 +167,31 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void norm_conv_kernel(
   }
 }
 
+template <typename T, int NG, int kRows>
+void launch_rows(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const void* ln_b,
+                 const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
+                 int64_t B, int64_t L, int64_t D, float eps, hipStream_t s) {
+  const int64_t rows_per_block = (int64_t)kWavesPerBlock * kRows;
+  dim3 grid((unsigned)((L + rows_per_block - 1) / rows_per_block), (unsigned)B);
+  hipLaunchKernelGGL((norm_conv_kernel<T, NG, kRows>), grid, dim3(kWavesPerBlock * kWave), 0, s,
+                     (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,
+                     (const T*)conv_b, (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
+}
+
+// Rows per wave: 16 by default (3/16 halo re-reads), 8 with HDCM_NORM_CONV_ROWS=8.
+int rows_per_wave() {
+  const char* v = getenv("HDCM_NORM_CONV_ROWS");
+  return (v && atoi(v) == 8) ? 8 : 16;
+}
+
 template <typename T, int NG>
 int launch_ng(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const void* ln_b,
               const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
               int64_t B, int64_t L, int64_t D, float eps, hipStream_t s) {
-  const int64_t rows_per_block = (int64_t)kWavesPerBlock * kRows;
-  dim3 grid((unsigned)((L + rows_per_block - 1) / rows_per_block), (unsigned)B);
-  hipLaunchKernelGGL((norm_conv_kernel<T, NG>), grid, dim3(kWavesPerBlock * kWave), 0, s,
-                     (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,
-                     (const T*)conv_b, (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
+  if (rows_per_wave() == 8)
+    launch_rows<T, NG, 8>(x, x_bs, x_rs, ln_w, ln_b, conv_w, conv_b, out, o_bs, o_rs, B, L, D, eps, s);
+  else
+    launch_rows<T, NG, 16>(x, x_bs, x_rs, ln_w, ln_b, conv_w, conv_b, out, o_bs, o_rs, B, L, D, eps, s);
   return hdcm_launch_status();
 }
 
@@ -220,7 +237,7 @@ extern "C" int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t
   const int E = 16 / esz;
   HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(D / E <= 12 * kWave, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 31, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(x_row_stride >= D && out_row_stride >= D, HDCM_EINVAL);
   HDCM_CHECK_ARG(x_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(x_batch_stride % E == 0 && out_batch_stride % E == 0, HDCM_EALIGN);

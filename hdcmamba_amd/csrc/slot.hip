@@ -36,7 +36,7 @@
 // GroupNorm needs only an in-lane sum and two cross-lane shuffles, and stores are
 // contiguous runs of 4 elements.  The state update S[dk][dv] += K~^T V is split across
 // the 4 waves by 16-column dv tiles and stays in MFMA accumulators; the rounded S_eff^T
-// is shared through a double-buffered LDS tile.
+// is shared through an LDS tile written while the next row tile is staged.
 #include <stdlib.h>
 
 #include "hdcm_common.h"
@@ -47,8 +47,8 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTargetWorkgroups = 512;
-constexpr int kGateWavesPerEU = 2;  // register budget for the gate kernel (waves per SIMD)
+constexpr int kTargetWorkgroups = 1024;
+constexpr int kGateWavesPerEU = 3;  // register budget: 3 waves per SIMD (3 workgroups per CU)
 constexpr int kMinSegTiles = 4;
 
 template <typename T>
@@ -56,53 +56,63 @@ struct TileOf {
   static constexpr int value = sizeof(T) == 2 ? 64 : 32;
 };
 
-// LDS tiles.  Row tiles [TC][HD] hold phi(q) and phi(k); transposed tiles [HD][TC] hold
-// (phi(k)*decay)^T and v^T; the S tile [HD][HD] holds S_eff^T.  Where a row spans a
-// multiple of 8 16-byte chunks the chunks are XOR-swizzled, chunk ^ ((row + row/8) % 8),
-// instead of padded: the transposed 2-byte stores of a wave (8 rows x 8 column groups)
-// then hit 32 distinct dwords, and 16-byte fragment reads of 16 consecutive rows hit
-// distinct bank groups.  Other row lengths are padded by one chunk.
+// LDS tiles of one row tile.  phi(q), phi(k) and S_eff^T feed the MFMAs through 16-byte
+// reads along the head dim; they are row-major with a pitch of HD plus one 16-byte chunk,
+// which puts the reads of 16 consecutive rows on distinct banks.  k~ = phi(k)*decay and v
+// feed P.V and the state update along the token dim.  For bf16 they stay row-major
+// (pitch HD+16, 16-byte stores) and are read with ds_read_tr16_b64, which hands each lane
+// 4 consecutive tokens of one column; for fp32 they are stored transposed, [HD][TC].
 template <typename T, int HD, int TC>
 struct Lds {
-  static constexpr int E = 16 / sizeof(T);  // elements per 16-byte chunk
-  static constexpr bool SW_R = (HD / E) % 8 == 0;
-  static constexpr bool SW_T = (TC / E) % 8 == 0;
-  static constexpr int PR = SW_R ? HD : HD + E;  // pitch of row tiles and of the S tile
-  static constexpr int PT = SW_T ? TC : TC + E;  // pitch of transposed tiles
-  static constexpr int tileR = TC * PR;
-  static constexpr int tileT = HD * PT;
-  static constexpr int oQ = 0;
-  static constexpr int oK = oQ + tileR;
-  static constexpr int oKt = oK + tileR;
-  static constexpr int oVt = oKt + tileT;
-  static constexpr int oS = oVt + tileT;
-  static constexpr int total = oS + HD * PR;
-  // the state pre-pass uses only the two transposed tiles
-  static constexpr int stKt = 0;
-  static constexpr int stVt = tileT;
-  static constexpr int stTotal = 2 * tileT;
-
-  __device__ static __forceinline__ int swz(int row, int col) {
-    return (((col / E) ^ ((row + (row >> 3)) & 7)) * E) + (col % E);
-  }
-  // element offset of (row, col) in a row tile / the S tile, and in a transposed tile
-  __device__ static __forceinline__ int r_at(int row, int col) {
-    return row * PR + (SW_R ? swz(row, col) : col);
-  }
-  __device__ static __forceinline__ int t_at(int row, int col) {
-    return row * PT + (SW_T ? swz(row, col) : col);
-  }
+  static constexpr bool TR = sizeof(T) == 2;
+  static constexpr int E = 16 / sizeof(T);
+  static constexpr int PQ = HD + E;
+  static constexpr int PV = TR ? HD + 16 : TC + E;
+  static constexpr int tileQ = TC * PQ;
+  static constexpr int tileV = TR ? TC * PV : HD * PV;
+  static constexpr int oQ = 0;             // phi(q)
+  static constexpr int oK = oQ + tileQ;    // phi(k)
+  static constexpr int oKd = oK + tileQ;   // k~ = phi(k) * gamma^(tlen-1-i)
+  static constexpr int oV = oKd + tileV;   // v
+  static constexpr int oS = oV + tileV;    // S_eff^T [HD][HD]
+  static constexpr int total = oS + HD * PQ;
+  // the state pre-pass uses only k~ and v
+  static constexpr int stKd = 0;
+  static constexpr int stV = tileV;
+  static constexpr int stTotal = 2 * tileV;
 };
 
-// Fragment of 8 consecutive columns col..col+7 of `row` (col a multiple of 8).
-template <typename T, int HD, int TC, bool TRANSPOSED>
-__device__ __forceinline__ void lds_frag8(Frag<T>& f, const T* tile, int row, int col) {
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+// Transpose read: within each 16-lane group, lane c supplies the address of 4 consecutive
+// 16-bit elements; lane x receives element x%4 of the chunks supplied by lanes x/4,
+// x/4+4, x/4+8 and x/4+12.
+__device__ __forceinline__ bf16x4_t lds_tr16(const bf16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4_t*)p);
+}
+
+// Head-dim fragment: columns col..col+7 of `row` of a PQ-pitched tile.
+template <typename T, int HD, int TC>
+__device__ __forceinline__ void frag_rows8(Frag<T>& f, const T* tile, int row, int col) {
+  frag_load8(f, tile + row * Lds<T, HD, TC>::PQ + col);
+}
+
+// Token-dim fragment of k~ or v: lane (x = lane%16, g = lane/16) receives, for head-dim
+// column d0 + x, tokens j0 + 4g + s in slots s = 0..3 and j0 + 16 + 4g + s - 4 in slots
+// 4..7 -- the slot order of the score fragments, used for every token contraction.
+template <typename T, int HD, int TC>
+__device__ __forceinline__ void frag_tok(Frag<T>& f, const T* tile, int d0, int j0, int lane) {
   using LD = Lds<T, HD, TC>;
-  auto at = [](int r, int c) { return TRANSPOSED ? LD::t_at(r, c) : LD::r_at(r, c); };
-  if constexpr (sizeof(T) == 2) {
-    frag_load8(f, tile + at(row, col));
+  const int x = lane & 15, g = lane >> 4;
+  if constexpr (LD::TR) {
+    // lane c of the group points at token j0 + 4g + c/4, columns d0 + 4*(c%4) .. +3
+    const T* p = tile + (j0 + 4 * g + (x >> 2)) * LD::PV + d0 + 4 * (x & 3);
+    const bf16x4_t lo = lds_tr16(p);
+    const bf16x4_t hi = lds_tr16(p + 16 * LD::PV);
+    f.v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   } else {
-    frag_load4x2(f, tile + at(row, col), tile + at(row, col + 4));
+    const T* p = tile + (d0 + x) * LD::PV + j0 + 4 * g;
+    frag_load4x2(f, p, p + 16);
   }
 }
 
@@ -209,8 +219,8 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
   using LD = Lds<T, HD, TC>;
   using TL = TileLoader<T, HD, TC, B0, NB>;
   constexpr int E = TL::E, GPR = TL::GPR;
-  T* sKt = sm + (STATE_ONLY ? LD::stKt : LD::oKt);
-  T* sVt = sm + (STATE_ONLY ? LD::stVt : LD::oVt);
+  T* sKd = sm + (STATE_ONLY ? LD::stKd : LD::oKd);
+  T* sV = sm + (STATE_ONLY ? LD::stV : LD::oV);
 #pragma unroll
   for (int it = 0; it < TL::NL; ++it) {
     const int idx = tid + kThreads * it;
@@ -218,29 +228,35 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
     const int rem = idx % (TC * GPR);
     const int i = rem / GPR, cg = rem % GPR;
     const bool ok = FULL || i < tlen;
-    if (blk == 0) {
+    if (blk == 0) {  // phi(q), row-major
       float f[E];
       unpack16<T>(raw[it], f);
 #pragma unroll
       for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
-      store16<T>(sm + LD::oQ + LD::r_at(i, cg * E), f);
-    } else if (blk == 1) {
-      float f[E];
+      store16<T>(sm + LD::oQ + i * LD::PQ + cg * E, f);
+    } else if (blk == 1) {  // phi(k) row-major; k~ = round(phi(k)) * gamma^(tlen-1-i)
+      float f[E], kdv[E];
       unpack16<T>(raw[it], f);
       const float kd = ok ? fexp2((float)(tlen - 1 - i) * lg2) : 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = rnd<T>(phi_f(f[e]));
-      if (!STATE_ONLY) {
-        float g[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) g[e] = ok ? f[e] : 0.f;
-        store16<T>(sm + LD::oK + LD::r_at(i, cg * E), g);
+      for (int e = 0; e < E; ++e) {
+        f[e] = ok ? rnd<T>(phi_f(f[e])) : 0.f;
+        kdv[e] = f[e] * kd;
       }
+      if (!STATE_ONLY) store16<T>(sm + LD::oK + i * LD::PQ + cg * E, f);
+      if constexpr (LD::TR) {
+        store16<T>(sKd + i * LD::PV + cg * E, kdv);
+      } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) sKt[LD::t_at(cg * E + e, i)] = from_f<T>(f[e] * kd);
-    } else {
+        for (int e = 0; e < E; ++e) sKd[(cg * E + e) * LD::PV + i] = from_f<T>(kdv[e]);
+      }
+    } else {  // v as stored
+      if constexpr (LD::TR) {
+        *reinterpret_cast<uint4*>(sV + i * LD::PV + cg * E) = raw[it];
+      } else {
 #pragma unroll
-      for (int e = 0; e < E; ++e) sVt[LD::t_at(cg * E + e, i)] = raw_elem<T>(raw[it], e);
+        for (int e = 0; e < E; ++e) sV[(cg * E + e) * LD::PV + i] = raw_elem<T>(raw[it], e);
+      }
     }
   }
 }
@@ -255,7 +271,7 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
 }
 
 template <typename T, int HD, int TC, bool HAS_W>
-__global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot_gate_kernel(
+__global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int dm, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
@@ -331,7 +347,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
             v[r] = cA * stA[ov][mt][r];
             if constexpr (HAS_W) v[r] += cW * stW[ov][mt][r];
           }
-          store4<T>(sm + LD::oS + LD::r_at(vt * 16 + l16, mt * 16 + kg * 4), v);
+          store4<T>(sm + LD::oS + (vt * 16 + l16) * LD::PQ + mt * 16 + kg * 4, v);
         }
       }
     }
@@ -354,7 +370,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
       for (int vt = 0; vt < NVT; ++vt) yacc[vt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       Frag<T> bq[NKS];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) lds_frag8<T, HD, TC, false>(bq[ks], sm + LD::oQ, iq, ks * 32 + kg * 8);
+      for (int ks = 0; ks < NKS; ++ks) frag_rows8<T, HD, TC>(bq[ks], sm + LD::oQ, iq, ks * 32 + kg * 8);
       // y^T += S_eff^T (phi(q)*gamma^iq)^T
       {
         const float qd = fexp2((float)iq * lg2);
@@ -364,7 +380,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
 #pragma unroll
           for (int vt = 0; vt < NVT; ++vt) {
             Frag<T> a;
-            lds_frag8<T, HD, TC, false>(a, sm + LD::oS, vt * 16 + l16, ks * 32 + kg * 8);
+            frag_rows8<T, HD, TC>(a, sm + LD::oS, vt * 16 + l16, ks * 32 + kg * 8);
             yacc[vt] = mma(a, bqd, yacc[vt]);
           }
         }
@@ -382,7 +398,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
               Frag<T> a;
-              lds_frag8<T, HD, TC, false>(a, sm + LD::oK, jt * 16 + l16, ks * 32 + kg * 8);
+              frag_rows8<T, HD, TC>(a, sm + LD::oK, jt * 16 + l16, ks * 32 + kg * 8);
               s = mma(a, bq[ks], s);
             }
           }
@@ -408,9 +424,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
           Frag<T> a;
-          const int row = vt * 16 + l16;
-          frag_load4x2(a, sm + LD::oVt + LD::t_at(row, 32 * t + kg * 4),
-                       sm + LD::oVt + LD::t_at(row, 32 * t + 16 + kg * 4));
+          frag_tok<T, HD, TC>(a, sm + LD::oV, vt * 16, 32 * t, lane);
           yacc[vt] = mma(a, pf, yacc[vt]);
         }
       }
@@ -456,7 +470,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
         Frag<T> bv[NJS];
 #pragma unroll
         for (int ks = 0; ks < NJS; ++ks)
-          lds_frag8<T, HD, TC, true>(bv[ks], sm + LD::oVt, vt * 16 + l16, ks * 32 + kg * 8);
+          frag_tok<T, HD, TC>(bv[ks], sm + LD::oV, vt * 16, 32 * ks, lane);
 #pragma unroll
         for (int mt = 0; mt < NVT; ++mt) {
           f32x4_t acc;
@@ -465,7 +479,7 @@ __global__ __launch_bounds__(kThreads, HD <= 64 ? kGateWavesPerEU : 1) void slot
 #pragma unroll
           for (int ks = 0; ks < NJS; ++ks) {
             Frag<T> a;
-            lds_frag8<T, HD, TC, true>(a, sm + LD::oKt, mt * 16 + l16, ks * 32 + kg * 8);
+            frag_tok<T, HD, TC>(a, sm + LD::oKd, mt * 16, 32 * ks, lane);
             acc = mma(a, bv[ks], acc);
           }
           if constexpr (HAS_W) stW[ov][mt] = acc;
@@ -547,14 +561,14 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
       Frag<T> bv[NJS];
 #pragma unroll
       for (int ks = 0; ks < NJS; ++ks)
-        lds_frag8<T, HD, TC, true>(bv[ks], sm + LD::stVt, vt * 16 + l16, ks * 32 + kg * 8);
+        frag_tok<T, HD, TC>(bv[ks], sm + LD::stV, vt * 16, 32 * ks, lane);
 #pragma unroll
       for (int mt = 0; mt < NVT; ++mt) {
         f32x4_t acc = st[ov][mt] * gt;
 #pragma unroll
         for (int ks = 0; ks < NJS; ++ks) {
           Frag<T> a;
-          lds_frag8<T, HD, TC, true>(a, sm + LD::stKt, mt * 16 + l16, ks * 32 + kg * 8);
+          frag_tok<T, HD, TC>(a, sm + LD::stKd, mt * 16, 32 * ks, lane);
           acc = mma(a, bv[ks], acc);
         }
         st[ov][mt] = acc;

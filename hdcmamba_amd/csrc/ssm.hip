@@ -29,15 +29,24 @@ constexpr int kPitch = kCh + 1;
 
 __device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : flog(1.0f + fexp(v)); }
 
-// Inclusive scan over the wave's lanes (row order) of (a, u) pairs.
-__device__ __forceinline__ void scan_pairs(float& a, float& u, int lane) {
+// Inclusive scans over the wave's lanes (row order) of NC independent (a, u) pair
+// streams, interleaved so the shuffles of different streams overlap.
+template <int NC>
+__device__ __forceinline__ void scan_pairs(float (&a)[NC], float (&u)[NC], int lane) {
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
-    const float ap = __shfl_up(a, off, kWave);
-    const float up = __shfl_up(u, off, kWave);
+    float ap[NC], up[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      ap[c] = __shfl_up(a[c], off, kWave);
+      up[c] = __shfl_up(u[c], off, kWave);
+    }
     if (lane >= off) {
-      u = a * up + u;
-      a = a * ap;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        u[c] = a[c] * up[c] + u[c];
+        a[c] = a[c] * ap[c];
+      }
     }
   }
 }
@@ -61,6 +70,15 @@ __global__ __launch_bounds__(kThreads) void ssm_tile_kernel(
 
   // Stage (a, u) pairs.  Rows past the tile or channels past ds get the identity (1, 0).
   uint4 rd[ITEMS], rx[ITEMS], rb[ITEMS];
+  // every item of this thread covers the same column group (kThreads is a multiple of GPR)
+  const int cg0 = tid % GPR;
+  float negA[E];
+  {
+    float al[E] = {};
+    if (cg0 * E < nch) load16<T>(A_log + c0 + cg0 * E, al);
+#pragma unroll
+    for (int e = 0; e < E; ++e) negA[e] = -fexp(al[e]);
+  }
 #pragma unroll
   for (int k = 0; k < ITEMS; ++k) {
     const int idx = tid + kThreads * k;
@@ -76,37 +94,48 @@ __global__ __launch_bounds__(kThreads) void ssm_tile_kernel(
     const int idx = tid + kThreads * k;
     const int i = idx / GPR, cg = idx % GPR;
     const bool ok = i < tlen && cg * E < nch;
-    float d[E], xv[E], bv[E], al[E] = {};
+    float d[E], xv[E], bv[E];
     unpack16<T>(rd[k], d);
     unpack16<T>(rx[k], xv);
     unpack16<T>(rb[k], bv);
-    if (ok) load16<T>(A_log + c0 + cg * E, al);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const float dt = softplus20(d[e]);
-      const float A = -fexp(al[e]);
-      sa[i * kPitch + cg * E + e] = ok ? fexp(dt * A) : 1.0f;
+      sa[i * kPitch + cg * E + e] = ok ? fexp(dt * negA[e]) : 1.0f;
       su[i * kPitch + cg * E + e] = ok ? dt * bv[e] * xv[e] : 0.0f;
     }
   }
   __syncthreads();
 
-  // Wave w scans channels w, w+4, ...; lane = row.
+  // Wave w scans channels w + 4*(k*kNC + c) for c < kNC, kNC at a time; lane = row.
+  // Channels past nch scan the identity pairs staged above and are never written.
+  constexpr int kNC = 4;
+  constexpr int kWaves = kThreads / kWave;
   const int64_t tb = (int64_t)b * ds;
-  for (int c = w; c < nch; c += kThreads / kWave) {
-    float a = sa[lane * kPitch + c];
-    float u = su[lane * kPitch + c];
-    scan_pairs(a, u, lane);
-    const int64_t ci = (tb + c0 + c) * ntiles + tile;  // [b][channel][tile]
-    if constexpr (!OUTPUT) {
-      if (lane == kWave - 1) {
-        tot_a[ci] = a;
-        tot_h[ci] = u;
+  for (int cb = w; cb < nch; cb += kWaves * kNC) {
+    float a[kNC], u[kNC];
+#pragma unroll
+    for (int c = 0; c < kNC; ++c) {
+      const int ch = cb + kWaves * c;
+      a[c] = ch < kCh ? sa[lane * kPitch + ch] : 1.0f;
+      u[c] = ch < kCh ? su[lane * kPitch + ch] : 0.0f;
+    }
+    scan_pairs<kNC>(a, u, lane);
+#pragma unroll
+    for (int c = 0; c < kNC; ++c) {
+      const int ch = cb + kWaves * c;
+      if (ch >= nch) continue;
+      const int64_t ci = (tb + c0 + ch) * ntiles + tile;  // [b][channel][tile]
+      if constexpr (!OUTPUT) {
+        if (lane == kWave - 1) {
+          tot_a[ci] = a[c];
+          tot_h[ci] = u[c];
+        }
+      } else {
+        const float h = u[c] + a[c] * hin[ci];
+        su[lane * kPitch + ch] = h;
+        if (h_final != nullptr && tile == ntiles - 1 && lane == tlen - 1) h_final[tb + c0 + ch] = h;
       }
-    } else {
-      const float h = u + a * hin[ci];
-      su[lane * kPitch + c] = h;
-      if (h_final != nullptr && tile == ntiles - 1 && lane == tlen - 1) h_final[tb + c0 + c] = h;
     }
   }
   if constexpr (OUTPUT) {
