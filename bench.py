@@ -50,6 +50,77 @@ def kernel_bytes(cfg, name):
     }[name]
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "slot_gate_lm_c4_traffic.md")
+TRAFFIC_KEY = "traffic_bytes_per_launch:"
+
+
+def _short_name(n):
+    n = n.replace("void ", "").replace("(anonymous namespace)::", "")
+    return n.split("(")[0]
+
+
+def pmc_summary(fetch_csv, write_csv, copy_bytes):
+    """Per-kernel HBM bytes per dispatch from two rocprofv3 --pmc runs (FETCH_SIZE and
+    WRITE_SIZE, KiB per dispatch).  Each counter is scaled by bytes / counter reading of the
+    runtime's copy kernel for the copy of known size (`copy_bytes`) in the same run.
+    Returns markdown text."""
+    import collections
+    import csv
+
+    def read(path, counter):
+        agg = collections.defaultdict(list)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    agg[_short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        return agg
+
+    def scale(agg, counter):
+        cands = [v for v in agg.get("__amd_rocclr_copyBuffer", []) if v > 0.25 * copy_bytes / 1024]
+        if not cands:
+            raise SystemExit(f"no copy kernel of ~{copy_bytes} bytes in the {counter} run")
+        return copy_bytes / (max(cands) * 1024)
+
+    fa, wa = read(fetch_csv, "FETCH_SIZE"), read(write_csv, "WRITE_SIZE")
+    ff, fw = scale(fa, "FETCH_SIZE"), scale(wa, "WRITE_SIZE")
+    lines = ["| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB per dispatch (scaled) |",
+             "|---|---:|---:|---:|---:|"]
+    out = {}
+    for k in sorted(set(fa) & set(wa), key=lambda k: -sum(fa[k]) / len(fa[k])):
+        f, w = sum(fa[k]) / len(fa[k]), sum(wa[k]) / len(wa[k])
+        out[k] = (f * ff + w * fw) * 1024
+        lines.append(f"| {k[:70]} | {len(fa[k])} | {f:.1f} | {w:.1f} | {out[k] / 1e6:.2f} |")
+    gate = [k for k in out if k.startswith("slot_gate_kernel")]
+    head = [f"copy calibration ({copy_bytes} bytes): FETCH_SIZE x {ff:.4f}, WRITE_SIZE x {fw:.4f}", ""]
+    if gate:
+        head += [f"{TRAFFIC_KEY} {round(out[gate[0]])}", ""]
+    return "\n".join(head + lines) + "\n"
+
+
+def stats_summary(stats_csv):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
+    import csv
+
+    with open(stats_csv) as f:
+        rows = list(csv.DictReader(f))
+    lines = ["| kernel | calls | avg us | share |", "|---|---:|---:|---:|"]
+    for r in rows:
+        lines.append(f"| {_short_name(r['Name'])[:70]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
+                     f"| {float(r['Percentage']):.1f}% |")
+    return "\n".join(lines) + "\n"
+
+
+def stored_traffic(workload):
+    """HBM bytes per slot_gate launch recorded by the counter runs for the L=32768 LM."""
+    if workload != "lm_c4" or not os.path.exists(TRAFFIC_SUMMARY):
+        return None
+    with open(TRAFFIC_SUMMARY) as f:
+        for line in f:
+            if line.startswith(TRAFFIC_KEY):
+                return int(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(model, ids_gpu, cfg, budget_s):
     """Time the CPU oracle on the same weights: all layers at a shorter sequence when the full
     one would exceed the budget; layers beyond the budget are extrapolated from the mean."""
@@ -97,7 +168,19 @@ def main():
     ap.add_argument("--workload", default="lm_c4", choices=["lm_c4", "lm_c3", "block_c2"])
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM traffic table of two rocprofv3 --pmc runs of this bench "
+                         "(FETCH_SIZE, WRITE_SIZE) and exit; needs no GPU")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="print the per-kernel table of a rocprofv3 --stats run and exit")
     args = ap.parse_args()
+    if args.stats_summary:
+        sys.stdout.write(stats_summary(args.stats_summary))
+        return
+    if args.pmc_summary:
+        # the residual-stream copy of the embedding output: B*L*d_model bf16 values
+        sys.stdout.write(pmc_summary(*args.pmc_summary, copy_bytes=32768 * 1024 * 2))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one MI355X (got --gpus {args.gpus}, WORLD_SIZE {world}); runs on "
@@ -148,7 +231,7 @@ def main():
     dom = "slot_gate"
     d = kernels[dom]
     roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": d["frac_hbm"], "traffic": None,
+                "frac": d["frac_hbm"], "traffic": stored_traffic(args.workload),
                 "bytes_per_launch": kernel_bytes(cfg, dom) * tokens}
     if "slot_state" in kernels:
         us = kernels["slot_state"]["us"] + kernels["slot_gate"]["us"]

@@ -39,6 +39,8 @@
 // is shared through an LDS tile written while the next row tile is staged.
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -186,27 +188,48 @@ struct TileLoader {
   static constexpr int E = Vec<T>::N;
   static constexpr int GPR = HD / E;
   static constexpr int NL = NB * TC * GPR / kThreads;
+  static constexpr int IPB = TC * GPR / kThreads;        // iterations per block
+  static constexpr bool SCALAR = (kThreads % GPR) == 0;  // row step per iteration is uniform
   static_assert((TC * GPR) % kThreads == 0, "tile block must be a multiple of the workgroup");
-  int64_t off[NL];  // element offset of each group relative to the tile's first row
-  int row[NL];
-  __device__ __forceinline__ TileLoader(int64_t prs, int dm, int tid) {
+  // With SCALAR, iteration it reads row tid/GPR + (it % IPB) * (kThreads/GPR) of block
+  // B0 + it/IPB at column group tid%GPR: one per-thread offset plus uniform strides.
+  int64_t base;
+  int row0;
+  int64_t prs;
+  int dm;
+  int64_t off[SCALAR ? 1 : NL];
+  int row[SCALAR ? 1 : NL];
+  __device__ __forceinline__ TileLoader(int64_t prs_, int dm_, int tid) : prs(prs_), dm(dm_) {
+    row0 = tid / GPR;
+    base = (int64_t)row0 * prs + (tid % GPR) * E;
+    if constexpr (!SCALAR) {
 #pragma unroll
-    for (int it = 0; it < NL; ++it) {
-      const int idx = tid + kThreads * it;
-      const int blk = B0 + (kThreads * it) / (TC * GPR);
-      const int rem = idx % (TC * GPR);
-      row[it] = rem / GPR;
-      off[it] = (int64_t)row[it] * prs + (blk - B0) * dm + (rem % GPR) * E;
+      for (int it = 0; it < NL; ++it) {
+        const int idx = tid + kThreads * it;
+        const int blk = B0 + (kThreads * it) / (TC * GPR);
+        const int rem = idx % (TC * GPR);
+        row[it] = rem / GPR;
+        off[it] = (int64_t)row[it] * prs + (blk - B0) * dm + (rem % GPR) * E;
+      }
     }
+  }
+  __device__ __forceinline__ int row_of(int it) const {
+    if constexpr (SCALAR) return row0 + (it % IPB) * (kThreads / GPR);
+    else return row[it];
+  }
+  __device__ __forceinline__ int64_t off_of(int it) const {
+    if constexpr (SCALAR)
+      return base + (int64_t)((it % IPB) * (kThreads / GPR)) * prs + (int64_t)(it / IPB) * dm;
+    else return off[it];
   }
   __device__ __forceinline__ void load(uint4 (&raw)[NL], const T* tile_base, int tlen) const {
     if (tlen == TC) {
 #pragma unroll
-      for (int it = 0; it < NL; ++it) raw[it] = ldg16(tile_base + off[it]);
+      for (int it = 0; it < NL; ++it) raw[it] = ldg16(tile_base + off_of(it));
     } else {
 #pragma unroll
       for (int it = 0; it < NL; ++it)
-        raw[it] = row[it] < tlen ? ldg16(tile_base + off[it]) : make_uint4(0, 0, 0, 0);
+        raw[it] = row_of(it) < tlen ? ldg16(tile_base + off_of(it)) : make_uint4(0, 0, 0, 0);
     }
   }
 };
@@ -358,12 +381,13 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     if (w < NIT) {
       const int it = w;
       const int iq = it * 16 + l16;
-      // gate values of this lane's output positions, loaded early
-      float gv[NVT][4];
+      // gate values of this lane's output positions, loaded early and kept as stored
+      typedef typename std::conditional<sizeof(T) == 2, uint2, float4>::type G4;
+      G4 graw[NVT];
       if (iq < tlen) {
         const T* grow = gatebase + (rowbase + p + iq) * prs + kg * 4;
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) load4<T>(grow + vt * 16, gv[vt]);
+        for (int vt = 0; vt < NVT; ++vt) graw[vt] = *reinterpret_cast<const G4*>(grow + vt * 16);
       }
       f32x4_t yacc[NVT];
 #pragma unroll
@@ -448,12 +472,13 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + kg * 4;
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
-          float o[4];
+          float gv[4], o[4];
+          load4<T>(reinterpret_cast<const T*>(&graw[vt]), gv);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int dv = vt * 16 + kg * 4 + r;
             const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
-            o[r] = yn * frcp(1.0f + fexp(-gv[vt][r]));
+            o[r] = yn * frcp(1.0f + fexp(-gv[r]));
           }
           store4<T>(orow + vt * 16, o);
         }
@@ -544,14 +569,18 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
 #pragma unroll
     for (int mt = 0; mt < NVT; ++mt) st[ov][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // Two tiles in flight: the per-tile MFMA work is short, so one tile of prefetch would
+  // leave each step waiting for a full memory round trip.
   const TL loader(prs, dm, tid);
-  uint4 raw[TL::NL];
-  loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
-  for (int p = p_begin; p < p_end; p += TC) {
+  uint4 raw0[TL::NL], raw1[TL::NL];
+  const T* tbase = colbase + rowbase * prs;
+  loader.load(raw0, tbase + (int64_t)p_begin * prs, min(TC, L - p_begin));
+  if (p_begin + TC < p_end) loader.load(raw1, tbase + (int64_t)(p_begin + TC) * prs, min(TC, L - p_begin - TC));
+  auto step = [&](uint4 (&raw)[TL::NL], int p) {
     const int tlen = min(TC, L - p);
     __syncthreads();
     stage_tile<T, HD, TC, 1, 2, true>(raw, sm, tlen, lg2, tid);
-    if (p + TC < p_end) loader.load(raw, colbase + (rowbase + p + TC) * prs, min(TC, L - p - TC));
+    if (p + 2 * TC < p_end) loader.load(raw, tbase + (int64_t)(p + 2 * TC) * prs, min(TC, L - p - 2 * TC));
     __syncthreads();
     const float gt = fexp2((float)tlen * lg2);
 #pragma unroll
@@ -574,6 +603,10 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
         st[ov][mt] = acc;
       }
     }
+  };
+  for (int p = p_begin; p < p_end; p += 2 * TC) {
+    step(raw0, p);
+    if (p + TC < p_end) step(raw1, p + TC);
   }
   float* u = U + (((int64_t)b * H + h) * nseg + seg) * HD * HD;
 #pragma unroll
@@ -602,7 +635,7 @@ __global__ __launch_bounds__(kThreads) void slot_scan_kernel(const float* __rest
   float a = S0 ? S0[bh * HD2 + e] : 0.f;
   const float* u = U + bh * nseg * HD2 + e;
   float* o = Ain + bh * nseg * HD2 + e;
-  constexpr int kU = 8;
+  constexpr int kU = 32;  // loads of a batch are all in flight before the recurrence uses them
   int s = 0;
   for (; s + kU <= nseg; s += kU) {
     float uu[kU];
