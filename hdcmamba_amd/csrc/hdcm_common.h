@@ -108,6 +108,38 @@ __device__ __forceinline__ float quad_group_sum(float v) {
   return v;
 }
 
+// softplus with the threshold 20 of F.softplus: x above it, log(1 + exp(x)) below.
+__device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : flog(1.0f + fexp(v)); }
+
+// One Hillis-Steele step of the (a, u) scan: combine with the pair fetched by the DPP
+// control CTRL; lanes whose source is out of range or masked off fetch the identity (1, 0).
+template <int CTRL, int ROW_MASK, int NC>
+__device__ __forceinline__ void scan_step_dpp(float (&a)[NC], float (&u)[NC]) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float ap = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(1.0f), __float_as_int(a[c]), CTRL, ROW_MASK, 0xf, false));
+    const float up = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(0.0f), __float_as_int(u[c]), CTRL, ROW_MASK, 0xf, false));
+    u[c] = a[c] * up + u[c];
+    a[c] = a[c] * ap;
+  }
+}
+
+// Inclusive scans over the wave's 64 lanes (lane order) of NC independent (a, u) pair
+// streams under (a1, u1) then (a2, u2) = (a1*a2, a2*u1 + u2), on DPP lane moves:
+// row_shr 1, 2, 4, 8 scan each 16-lane row; row_bcast 15 then folds row 0 into row 1 and
+// row 2 into row 3, and row_bcast 31 folds rows 0-1 into rows 2-3.
+template <int NC>
+__device__ __forceinline__ void scan_pairs(float (&a)[NC], float (&u)[NC]) {
+  scan_step_dpp<0x111, 0xf>(a, u);  // row_shr:1
+  scan_step_dpp<0x112, 0xf>(a, u);  // row_shr:2
+  scan_step_dpp<0x114, 0xf>(a, u);  // row_shr:4
+  scan_step_dpp<0x118, 0xf>(a, u);  // row_shr:8
+  scan_step_dpp<0x142, 0xa>(a, u);  // row_bcast:15 into rows 1 and 3
+  scan_step_dpp<0x143, 0xc>(a, u);  // row_bcast:31 into rows 2 and 3
+}
+
 // ------------------------------------------------------------- MFMA fragments
 // A 16x16 MFMA tile step contracts K=32.  A lane owns 8 contraction slots s=0..7 of
 // one row (A operand) or column (B operand).  For bf16 the 8 slots feed one

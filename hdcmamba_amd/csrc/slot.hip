@@ -222,14 +222,15 @@ struct TileLoader {
       return base + (int64_t)((it % IPB) * (kThreads / GPR)) * prs + (int64_t)(it / IPB) * dm;
     else return off[it];
   }
+  // Always NL loads, whatever tlen (>= 1): a fixed count per tile keeps the compiler's
+  // memory-counter waits exact instead of draining every outstanding load.  Rows past the
+  // tile read row 0 of the tile and are zeroed when staged.
   __device__ __forceinline__ void load(uint4 (&raw)[NL], const T* tile_base, int tlen) const {
-    if (tlen == TC) {
 #pragma unroll
-      for (int it = 0; it < NL; ++it) raw[it] = ldg16(tile_base + off_of(it));
-    } else {
-#pragma unroll
-      for (int it = 0; it < NL; ++it)
-        raw[it] = row_of(it) < tlen ? ldg16(tile_base + off_of(it)) : make_uint4(0, 0, 0, 0);
+    for (int it = 0; it < NL; ++it) {
+      const int r = row_of(it);
+      const int64_t off = off_of(it);
+      raw[it] = ldg16(tile_base + (r < tlen ? off : off - (int64_t)r * prs));
     }
   }
 };
@@ -274,11 +275,12 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
         for (int e = 0; e < E; ++e) sKd[(cg * E + e) * LD::PV + i] = from_f<T>(kdv[e]);
       }
     } else {  // v as stored
+      const uint4 vv = ok ? raw[it] : make_uint4(0, 0, 0, 0);
       if constexpr (LD::TR) {
-        *reinterpret_cast<uint4*>(sV + i * LD::PV + cg * E) = raw[it];
+        *reinterpret_cast<uint4*>(sV + i * LD::PV + cg * E) = vv;
       } else {
 #pragma unroll
-        for (int e = 0; e < E; ++e) sV[(cg * E + e) * LD::PV + i] = raw_elem<T>(raw[it], e);
+        for (int e = 0; e < E; ++e) sV[(cg * E + e) * LD::PV + i] = raw_elem<T>(vv, e);
       }
     }
   }
@@ -347,6 +349,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   const TL loader(prs, dm, tid);
   uint4 raw[TL::NL];
   loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
+
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
     __syncthreads();
@@ -374,7 +377,11 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         }
       }
     }
-    if (p + TC < p_end) loader.load(raw, colbase + (rowbase + p + TC) * prs, min(TC, L - p - TC));
+    {
+      // next tile, or this tile again (already in cache) after the last: a fixed load count
+      const int pn = p + TC < p_end ? p + TC : p;
+      loader.load(raw, colbase + (rowbase + pn) * prs, min(TC, L - pn));
+    }
     __syncthreads();
 
     // ---- outputs for query rows 16*w .. 16*w+15
@@ -524,6 +531,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         }
       }
     }
+
   }
 
   if (S_final != nullptr && seg == nseg - 1) {
@@ -542,7 +550,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
 
 // Per (segment, head, batch): U_s = sum_{j in segment} gamma^(end-1-j) k~_j^T v_j.
 template <typename T, int HD, int TC>
-__global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restrict__ projs,
+__global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(const T* __restrict__ projs,
                                                               int64_t prs, int q_col, int dm,
                                                               int L, const T* __restrict__ gamma,
                                                               int seg_tiles, int nseg,
@@ -571,16 +579,23 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
 
   // Two tiles in flight: the per-tile MFMA work is short, so one tile of prefetch would
   // leave each step waiting for a full memory round trip.
+  // Two tiles in flight: the per-tile MFMA work is short, so one tile of prefetch would
+  // leave each step waiting for a full memory round trip.  Prefetches past the segment
+  // re-read the current tile, and the loop body always runs both steps (tlen = 0 makes a
+  // step a no-op: zero tile, gamma^0 = 1), so every path issues the same loads in the same
+  // order and the compiler's memory-counter waits stay exact.
   const TL loader(prs, dm, tid);
   uint4 raw0[TL::NL], raw1[TL::NL];
   const T* tbase = colbase + rowbase * prs;
+  const int p1 = p_begin + TC < p_end ? p_begin + TC : p_begin;
   loader.load(raw0, tbase + (int64_t)p_begin * prs, min(TC, L - p_begin));
-  if (p_begin + TC < p_end) loader.load(raw1, tbase + (int64_t)(p_begin + TC) * prs, min(TC, L - p_begin - TC));
-  auto step = [&](uint4 (&raw)[TL::NL], int p) {
-    const int tlen = min(TC, L - p);
+  loader.load(raw1, tbase + (int64_t)p1 * prs, min(TC, L - p1));
+
+  auto step = [&](uint4 (&raw)[TL::NL], int p, int tlen) {
     __syncthreads();
     stage_tile<T, HD, TC, 1, 2, true>(raw, sm, tlen, lg2, tid);
-    if (p + 2 * TC < p_end) loader.load(raw, tbase + (int64_t)(p + 2 * TC) * prs, min(TC, L - p - 2 * TC));
+    const int pn = p + 2 * TC < p_end ? p + 2 * TC : p;
+    loader.load(raw, tbase + (int64_t)pn * prs, min(TC, L - pn));
     __syncthreads();
     const float gt = fexp2((float)tlen * lg2);
 #pragma unroll
@@ -605,8 +620,9 @@ __global__ __launch_bounds__(kThreads) void slot_state_kernel(const T* __restric
     }
   };
   for (int p = p_begin; p < p_end; p += 2 * TC) {
-    step(raw0, p);
-    if (p + TC < p_end) step(raw1, p + TC);
+    step(raw0, p, min(TC, L - p));
+    const bool second = p + TC < p_end;
+    step(raw1, second ? p + TC : p, second ? min(TC, L - p - TC) : 0);
   }
   float* u = U + (((int64_t)b * H + h) * nseg + seg) * HD * HD;
 #pragma unroll

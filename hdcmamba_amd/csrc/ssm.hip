@@ -27,30 +27,6 @@ constexpr int kCh = 64;        // channels per workgroup
 constexpr int kThreads = 256;  // 4 waves, 16 channels each
 constexpr int kPitch = kCh + 1;
 
-__device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : flog(1.0f + fexp(v)); }
-
-// Inclusive scans over the wave's lanes (row order) of NC independent (a, u) pair
-// streams, interleaved so the shuffles of different streams overlap.
-template <int NC>
-__device__ __forceinline__ void scan_pairs(float (&a)[NC], float (&u)[NC], int lane) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    float ap[NC], up[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      ap[c] = __shfl_up(a[c], off, kWave);
-      up[c] = __shfl_up(u[c], off, kWave);
-    }
-    if (lane >= off) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        u[c] = a[c] * up[c] + u[c];
-        a[c] = a[c] * ap[c];
-      }
-    }
-  }
-}
-
 template <typename T, bool OUTPUT>
 __global__ __launch_bounds__(kThreads) void ssm_tile_kernel(
     const T* __restrict__ projs, int64_t prs, const T* __restrict__ A_log,
@@ -120,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void ssm_tile_kernel(
       a[c] = ch < kCh ? sa[lane * kPitch + ch] : 1.0f;
       u[c] = ch < kCh ? su[lane * kPitch + ch] : 0.0f;
     }
-    scan_pairs<kNC>(a, u, lane);
+    scan_pairs<kNC>(a, u);
 #pragma unroll
     for (int c = 0; c < kNC; ++c) {
       const int ch = cb + kWaves * c;
