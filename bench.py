@@ -160,12 +160,66 @@ def cpu_baseline(model, ids_gpu, cfg, budget_s):
             "sample": sample, "cpu_model": _cpu_model(), "seconds_measured": round(time.perf_counter() - t_start, 2)}
 
 
+def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
+    """Prefill, then time decode steps (B tokens per step) replayed from the captured graph."""
+    B, L = cfg["B"], cfg["L"]
+    steps = args.steps if args.steps != 10 else 128
+    warm = max(args.warmup, 2)
+    lm = make_lm("lm_c5").to(torch.bfloat16).to(dev)
+    ids = lm_input("lm_c5", B=B, L=L + warm + steps + 1).to(dev)
+    with torch.no_grad():
+        lm.prefill(ids[:, :256])  # warm the prefill kernels and GEMM handles
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _, states = lm.prefill(ids[:, :L])
+        torch.cuda.synchronize()
+        t_prefill = time.perf_counter() - t0
+        runner = lm if args.eager else lm.capture_decode(states)
+        step = (lambda tok: lm.step(tok, states)) if args.eager else runner.step
+        for t in range(warm):
+            step(ids[:, L + t].contiguous())
+        torch.cuda.synchronize()
+        toks = [ids[:, L + warm + t].contiguous() for t in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for tok in toks:
+            step(tok)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+    # bytes one step must move: every parameter once (the tied head counted once) plus the
+    # carried states (slot: read S_prev, read+write S_intra; SSM: read+write h; conv history)
+    param_bytes = sum(p.numel() * p.element_size() for p in lm.parameters())
+    st = states[0]
+    state_bytes = len(states) * (3 * st.S_prev.numel() * 4 + 2 * st.h.numel() * 4 + 2 * st.conv.numel() * 2)
+    ms = sec / steps * 1e3
+    gbs = (param_bytes + state_bytes) / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "decode tokens/sec on 1 MI355X, B=16 after an L=8192 prefill",
+        "value": round(B * steps / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: uniform random token ids, random-init weights",
+        "config": {"workload": "48-layer d_model=2048 HdcMamba LM, prefill B=16 L=8192 then single-token decode",
+                   "d_model": 2048, "d_state": 128, "num_heads": 32, "chunk": 64, "layers": 48, "vocab": 50304,
+                   "global_batch": B, "prefill_len": L, "graph": not args.eager},
+        "roofline": {"kernel": "whole decode step", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": param_bytes + state_bytes},
+        "prefill_tokens_per_s": round(B * L / t_prefill, 1),
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="lm_c4", choices=["lm_c4", "lm_c3", "block_c2"])
+    ap.add_argument("--workload", default="lm_c4", choices=["lm_c4", "lm_c3", "block_c2", "lm_c5_decode"],
+                    help="lm_c5_decode: 48-layer d_model=2048 LM, prefill B=16 x 8192, then timed "
+                         "single-token decode steps (a separate measurement, not the headline line)")
+    ap.add_argument("--eager", action="store_true", help="lm_c5_decode: step from Python instead of "
+                    "replaying the captured decode graph")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -193,6 +247,8 @@ def main():
     from hdcmamba_amd import _ops
 
     dev = torch.device("cuda:0")
+    if args.workload == "lm_c5_decode":
+        return decode_bench(args, torch, WORKLOADS["lm_c5"], make_lm, lm_input, dev)
     cfg = dict(WORKLOADS[args.workload])
     cfg["dtype_name"] = "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32"
     if args.workload.startswith("lm"):

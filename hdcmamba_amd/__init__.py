@@ -3,12 +3,13 @@
 Public names match the reference package (hdcmamba/__init__.py:1-13).
 """
 from .model import (
+    BlockState,
     FusedNormConv1dFunction,
     HdcMamba9v3Block,
     HdcMamba9v3Model,
     fused_norm_conv1d_trainable,
 )
-from .lm import HdcMambaLM
+from .lm import DecodeGraph, HdcMambaLM
 
 __all__ = [
     "HdcMamba9v3Block",
@@ -16,4 +17,6 @@ __all__ = [
     "FusedNormConv1dFunction",
     "fused_norm_conv1d_trainable",
     "HdcMambaLM",
+    "BlockState",
+    "DecodeGraph",
 ]

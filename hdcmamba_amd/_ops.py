@@ -37,6 +37,14 @@ _PROTOS = {
                                    c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_rowln_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                c_int64, c_float, c_int, c_void_p]),
+    "hdcm_norm_conv_step_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float, c_int,
+                                        c_void_p]),
+    "hdcm_mixer_step_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_float,
+                                    c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                    c_int, c_void_p]),
+    "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
 }
 
 _lib = None
@@ -243,3 +251,65 @@ def layer_norm(x, w=None, b=None, eps=1e-5, out=None):
         rows, W, float(eps), _dtype(x), _stream(x)))
     timer.end("rowln", ev)
     return out
+
+
+# ----------------------------------------------------------------------------- decode step
+def norm_conv_step(x, ln_w, ln_b, conv_w, conv_b, eps, hist, out=None):
+    """One token per batch row: x [B,D] -> out [B,D]; hist [B,3,D] (raw previous rows,
+    x.dtype) is shifted in place."""
+    _on_gpu(x, hist)
+    B, D = x.shape
+    ln_w = _same(ln_w, x, "ln_w")
+    ln_b = _same(ln_b, x, "ln_b")
+    conv_b = _same(conv_b, x, "conv_b")
+    conv_w = _same(conv_w.reshape(D, 4), x, "conv_w")
+    if hist.dtype != x.dtype or not hist.is_contiguous() or tuple(hist.shape) != (B, 3, D):
+        raise RuntimeError("norm_conv_step: hist must be a contiguous [B,3,D] tensor of x's dtype")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if out is None:
+        out = torch.empty(B, D, device=x.device, dtype=x.dtype)
+    ev = timer.begin("norm_conv_step")
+    _check("hdcm_norm_conv_step_fwd", lib().hdcm_norm_conv_step_fwd(
+        x.data_ptr(), x.stride(0), ln_w.data_ptr(), ln_b.data_ptr(), conv_w.data_ptr(), conv_b.data_ptr(),
+        hist.data_ptr(), out.data_ptr(), out.stride(0), B, D, float(eps), _dtype(x), _stream(x)))
+    timer.end("norm_conv_step", ev)
+    return out
+
+
+def mixer_step(projs, A_log, d_state, q_col, gamma, gn_w, gn_b, gn_eps, h, S_prev, S_intra, pos, chunk,
+               out, d_model, num_heads, y_col=0, g_col=None, pos_dev=None):
+    """One token per batch row of the SSM and the slot memory + GroupNorm gate.
+    projs [B,P]; h [B,ds], S_prev / S_intra [B,H,hd,hd] fp32 contiguous, updated in place;
+    pos = token offset in its chunk (or, with pos_dev, an int32 device scalar holding it).
+    Writes out[:, y_col:y_col+ds] and out[:, g_col:g_col+dm]."""
+    _on_gpu(projs, out, h, S_prev, S_intra)
+    B = projs.shape[0]
+    if g_col is None:
+        g_col = y_col + d_state
+    hd = d_model // num_heads
+    for t, shape, name in ((h, (B, d_state), "h"), (S_prev, (B, num_heads, hd, hd), "S_prev"),
+                           (S_intra, (B, num_heads, hd, hd), "S_intra")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise RuntimeError(f"mixer_step: {name} must be a contiguous fp32 tensor of shape {shape}")
+    A_log = _same(A_log, projs, "A_log")
+    gamma = _same(gamma, projs, "gamma")
+    gn_w = _same(gn_w, projs, "gn_w")
+    gn_b = _same(gn_b, projs, "gn_b")
+    ev = timer.begin("mixer_step")
+    _check("hdcm_mixer_step_fwd", lib().hdcm_mixer_step_fwd(
+        projs.data_ptr(), _rows2d(projs, "projs"), q_col, A_log.data_ptr(), h.data_ptr(), gamma.data_ptr(),
+        S_prev.data_ptr(), S_intra.data_ptr(), int(pos), None if pos_dev is None else pos_dev.data_ptr(),
+        int(chunk), gn_w.data_ptr(), gn_b.data_ptr(),
+        float(gn_eps), out.data_ptr(), _rows2d(out, "out"), y_col, g_col, B, d_model, d_state, num_heads,
+        _dtype(projs), _stream(projs)))
+    timer.end("mixer_step", ev)
+    return out
+
+
+def chunk_pos_advance(pos_dev, chunk):
+    """pos_dev (int32 device scalar) <- (pos_dev + 1) mod chunk, on the current stream."""
+    _on_gpu(pos_dev)
+    if pos_dev.dtype != torch.int32 or pos_dev.numel() != 1:
+        raise RuntimeError("chunk_pos_advance: pos_dev must be a one-element int32 tensor")
+    _check("hdcm_chunk_pos_advance", lib().hdcm_chunk_pos_advance(pos_dev.data_ptr(), int(chunk), _stream(pos_dev)))

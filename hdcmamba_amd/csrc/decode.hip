@@ -1,0 +1,301 @@
+// Recurrent single-token step of the HdcMamba block for gfx950 (prefill -> decode).
+//
+// A prefill leaves, per block: the last three block-input rows (the conv history), the SSM
+// state h [B,ds] and the slot state at a chunk boundary.  Each decode step then advances
+// one token per batch row with the same semantics as the chunked forward
+// (hdcmamba/model.py:22-72, 175-233, 236-295):
+//
+//   norm_conv_step:  u = LN(x_t); out = sum_k u_{t-3+k} w_k + b, rows before the sequence
+//                    start having u = ln_b (the LayerNorm of a zero row); the history keeps
+//                    raw rows and is shifted in place.
+//   mixer_step:      SSM      h = exp(dt*A) h + dt*b*x,  y_ssm = h          (fp32 state)
+//                    slot     the weight of (t, j) is gamma^(t-j) inside t's chunk and
+//                             gamma^(t-j-1) across chunks, so with c = t mod C
+//                               S_intra <- gamma S_intra + phi(k_t)^T v_t
+//                               y_t      = phi(q_t) (S_intra + gamma^c S_prev)
+//                             and at the chunk's last token
+//                               S_prev  <- gamma^C S_prev + S_intra,  S_intra <- 0
+//                    then GroupNorm over the head's hd values and the sigmoid gate, written
+//                    next to y_ssm in the `combined` row.
+//
+// Decode is weight- and state-bandwidth bound (the GEMMs around it read every weight once
+// per step), so these kernels are simple: one workgroup per batch row (norm_conv_step) and
+// one per (head, batch) plus one per batch for the SSM channels (mixer_step).
+#include "hdcm_common.h"
+
+using namespace hdcm;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// Sum of N values per thread over the workgroup; every thread receives the totals.
+template <int N>
+__device__ __forceinline__ void block_sum(float (&v)[N], float* red) {
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+#pragma unroll
+  for (int n = 0; n < N; ++n) v[n] = wave_sum(v[n]);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) red[w * N + n] = v[n];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) s += red[k * N + n];
+    v[n] = s;
+  }
+}
+
+// One workgroup per batch row; thread t owns 16-byte column groups t, t+256, ...
+template <typename T, int NG>
+__global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
+    const T* __restrict__ x, int64_t x_rs, const T* __restrict__ ln_w, const T* __restrict__ ln_b,
+    const T* __restrict__ conv_w, const T* __restrict__ conv_b, T* __restrict__ hist,
+    T* __restrict__ out, int64_t o_rs, int D, float eps) {
+  constexpr int E = Vec<T>::N;
+  __shared__ float red[kWaves * 8];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int G = D / E;
+  // rows 0..2: history (oldest first), row 3: the new token
+  const T* rows[4] = {hist + ((int64_t)b * 3 + 0) * D, hist + ((int64_t)b * 3 + 1) * D,
+                      hist + ((int64_t)b * 3 + 2) * D, x + (int64_t)b * x_rs};
+  float r[4][NG][E];
+  float st[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st[n] = 0.f;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = tid + kThreads * i;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (g < G) load16<T>(rows[k] + g * E, r[k][i]);
+      else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) r[k][i][e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        st[2 * k] += r[k][i][e];
+        st[2 * k + 1] += r[k][i][e] * r[k][i][e];
+      }
+    }
+  }
+  block_sum<8>(st, red);
+  float mean[4], rstd[4];
+  const float invD = 1.0f / (float)D;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    mean[k] = st[2 * k] * invD;
+    const float var = fmaxf(st[2 * k + 1] * invD - mean[k] * mean[k], 0.f);
+    rstd[k] = rsqrtf(var + eps);
+  }
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = tid + kThreads * i;
+    if (g >= G) continue;
+    float w[E], bb[E], cb[E], cw[4 * E], o[E];
+    load16<T>(ln_w + g * E, w);
+    load16<T>(ln_b + g * E, bb);
+    load16<T>(conv_b + g * E, cb);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)g * E * 4 + k * E, cw + k * E);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float acc = cb[e];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += ((r[k][i][e] - mean[k]) * rstd[k] * w[e] + bb[e]) * cw[4 * e + k];
+      o[e] = acc;
+    }
+    store16<T>(out + (int64_t)b * o_rs + g * E, o);
+    // shift the history: rows 1, 2 and the new token become rows 0, 1, 2
+#pragma unroll
+    for (int k = 0; k < 3; ++k) store16<T>(hist + ((int64_t)b * 3 + k) * D + g * E, r[k + 1][i]);
+  }
+}
+
+__device__ __forceinline__ float phi_f(float z) { return fexp(fminf(z, 0.f)) + fmaxf(z, 0.f); }
+
+// grid (H + 1, B): x < H is head x's slot step, x == H the SSM channels of batch row b.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mixer_step_kernel(
+    const T* __restrict__ projs, int64_t prs, int q_col, int dm, int hd, const T* __restrict__ gamma,
+    float* __restrict__ S_prev, float* __restrict__ S_intra, int c_arg, const int* __restrict__ c_dev, int C,
+    const T* __restrict__ gn_w,
+    const T* __restrict__ gn_b, float gn_eps, const T* __restrict__ A_log, float* __restrict__ hs,
+    int ds, T* __restrict__ out, int64_t ors, int y_col, int g_col) {
+  __shared__ float sq[128], sk[128], sv[128], sy[kThreads];
+  __shared__ float red[kWaves * 2];
+  const int tid = threadIdx.x, b = blockIdx.y, H = gridDim.x - 1;
+  const T* row = projs + (int64_t)b * prs;
+  T* orow = out + (int64_t)b * ors;
+
+  if ((int)blockIdx.x == H) {  // SSM: h = exp(dt*A) h + dt*b*x
+    for (int ch = tid; ch < ds; ch += kThreads) {
+      const float dt = softplus20(to_f<T>(row[ch]));
+      const float a = fexp(-dt * fexp(to_f<T>(A_log[ch])));
+      const float u = dt * to_f<T>(row[2 * ds + ch]) * to_f<T>(row[ds + ch]);
+      float* hp = hs + (int64_t)b * ds + ch;
+      const float h = a * *hp + u;
+      *hp = h;
+      orow[y_col + ch] = from_f<T>(h);
+    }
+    return;
+  }
+
+  const int h = blockIdx.x;
+  // chunk offset: from device memory when the step runs inside a captured graph
+  const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
+  const float g = to_f<T>(gamma[h]);
+  const float lg2 = log2f(g);
+  const T* q = row + q_col + h * hd;
+  if (tid < hd) {
+    // phi(q), phi(k) rounded to the activation dtype as in the chunked kernels' operands
+    sq[tid] = rnd<T>(phi_f(to_f<T>(q[tid])));
+    sk[tid] = rnd<T>(phi_f(to_f<T>(q[dm + tid])));
+    sv[tid] = to_f<T>(q[2 * dm + tid]);
+  }
+  __syncthreads();
+
+  // thread (rg, j): column j of the state, rows rg, rg + RG, ...
+  const int RG = kThreads / hd;
+  const int rg = tid / hd, j = tid % hd;
+  const bool act = rg < RG;
+  const bool first = c == 0, last = c == C - 1;
+  const float gc = fexp2((float)c * lg2), gC = fexp2((float)C * lg2);
+  float acc = 0.f;
+  if (act) {
+    const int64_t base = (((int64_t)b * H + h) * hd) * hd + j;
+    const float vj = sv[j];
+    for (int i = rg; i < hd; i += RG) {
+      const int64_t e = base + (int64_t)i * hd;
+      const float sp = S_prev[e];
+      const float si = (first ? 0.f : g * S_intra[e]) + sk[i] * vj;
+      acc += sq[i] * (si + gc * sp);
+      if (last) {
+        S_prev[e] = gC * sp + si;
+        S_intra[e] = 0.f;
+      } else {
+        S_intra[e] = si;
+      }
+    }
+  }
+  sy[tid] = acc;
+  __syncthreads();
+  float y = 0.f;
+  if (tid < hd) {
+    for (int k = 0; k < RG; ++k) y += sy[k * hd + tid];
+  }
+  // GroupNorm over the head's hd values, then the gate
+  float st[2] = {tid < hd ? y : 0.f, tid < hd ? y * y : 0.f};
+  block_sum<2>(st, red);
+  const float mean = st[0] / (float)hd;
+  const float var = fmaxf(st[1] / (float)hd - mean * mean, 0.f);
+  const float rinv = rsqrtf(var + gn_eps);
+  if (tid < hd) {
+    const int col = h * hd + tid;
+    const float gate = to_f<T>(row[q_col + 3 * dm + col]);
+    const float yn = (y - mean) * rinv * to_f<T>(gn_w[col]) + to_f<T>(gn_b[col]);
+    orow[g_col + col] = from_f<T>(yn * frcp(1.0f + fexp(-gate)));
+  }
+}
+
+__global__ void chunk_pos_advance_kernel(int* pos, int C) {
+  if (threadIdx.x == 0) {
+    const int p = *pos + 1;
+    *pos = p == C ? 0 : p;
+  }
+}
+
+template <typename T>
+int launch_norm_conv_step(const void* x, int64_t x_rs, const void* ln_w, const void* ln_b,
+                          const void* conv_w, const void* conv_b, void* hist, void* out, int64_t o_rs,
+                          int64_t B, int64_t D, float eps, hipStream_t s) {
+  constexpr int E = Vec<T>::N;
+  const int64_t G = D / E;
+  const int ng = (int)((G + kThreads - 1) / kThreads);
+#define HDCM_NCS_CASE(N)                                                                             \
+  if (ng == N) {                                                                                     \
+    hipLaunchKernelGGL((norm_conv_step_kernel<T, N>), dim3((unsigned)B), dim3(kThreads), 0, s,      \
+                       (const T*)x, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,          \
+                       (const T*)conv_b, (T*)hist, (T*)out, o_rs, (int)D, eps);                      \
+    return hdcm_launch_status();                                                                     \
+  }
+  HDCM_NCS_CASE(1)
+  HDCM_NCS_CASE(2)
+  HDCM_NCS_CASE(3)
+  HDCM_NCS_CASE(4)
+#undef HDCM_NCS_CASE
+  return HDCM_EUNSUPPORTED;
+}
+
+}  // namespace
+
+extern "C" int hdcm_norm_conv_step_fwd(const void* x, int64_t x_row_stride, const void* ln_w,
+                                       const void* ln_b, const void* conv_w, const void* conv_b,
+                                       void* hist, void* out, int64_t out_row_stride, int64_t B,
+                                       int64_t D, float eps, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(x && ln_w && ln_b && conv_w && conv_b && hist && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(B >= 0 && D > 0 && x_row_stride >= D && out_row_stride >= D, HDCM_EINVAL);
+  const int E = 16 / hdcm_elt_size(dtype);
+  HDCM_CHECK_ARG(D % E == 0 && x_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(x) && hdcm_aligned16(out) && hdcm_aligned16(hist) && hdcm_aligned16(ln_w) &&
+                     hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w) && hdcm_aligned16(conv_b),
+                 HDCM_EALIGN);
+  HDCM_CHECK_ARG(D / E <= 4 * kThreads && B <= 65535, HDCM_EUNSUPPORTED);
+  if (B == 0) return HDCM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HDCM_F32)
+    return launch_norm_conv_step<float>(x, x_row_stride, ln_w, ln_b, conv_w, conv_b, hist, out,
+                                        out_row_stride, B, D, eps, s);
+  return launch_norm_conv_step<bf16_t>(x, x_row_stride, ln_w, ln_b, conv_w, conv_b, hist, out,
+                                       out_row_stride, B, D, eps, s);
+}
+
+extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col,
+                                   const void* A_log, float* h, const void* gamma, float* S_prev,
+                                   float* S_intra, int64_t pos, const int32_t* pos_dev, int64_t C,
+                                   const void* gn_w,
+                                   const void* gn_b, float gn_eps, void* out, int64_t out_row_stride,
+                                   int64_t y_col, int64_t g_col, int64_t B, int64_t dm, int64_t ds,
+                                   int64_t H, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(projs && A_log && h && gamma && S_prev && S_intra && gn_w && gn_b && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(B >= 0 && dm > 0 && ds > 0 && H > 0 && dm % H == 0 && C > 0, HDCM_EINVAL);
+  HDCM_CHECK_ARG(pos >= 0 && pos < C, HDCM_EINVAL);
+  HDCM_CHECK_ARG(q_col >= 3 * ds && proj_row_stride >= q_col + 4 * dm, HDCM_EINVAL);
+  HDCM_CHECK_ARG(y_col >= 0 && g_col >= 0 && out_row_stride >= y_col + ds && out_row_stride >= g_col + dm,
+                 HDCM_EINVAL);
+  const int64_t hd = dm / H;
+  HDCM_CHECK_ARG(hd <= 128 && H < 65535 && B <= 65535 && proj_row_stride < ((int64_t)1 << 31),
+                 HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(C < ((int64_t)1 << 24), HDCM_EUNSUPPORTED);
+  if (B == 0) return HDCM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(H + 1), (unsigned)B);
+  if (dtype == HDCM_F32)
+    hipLaunchKernelGGL((mixer_step_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs,
+                       proj_row_stride, (int)q_col, (int)dm, (int)hd, (const float*)gamma, S_prev, S_intra,
+                       (int)pos, (const int*)pos_dev, (int)C, (const float*)gn_w, (const float*)gn_b, gn_eps,
+                       (const float*)A_log, h, (int)ds, (float*)out, out_row_stride, (int)y_col,
+                       (int)g_col);
+  else
+    hipLaunchKernelGGL((mixer_step_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs,
+                       proj_row_stride, (int)q_col, (int)dm, (int)hd, (const bf16_t*)gamma, S_prev,
+                       S_intra, (int)pos, (const int*)pos_dev, (int)C, (const bf16_t*)gn_w, (const bf16_t*)gn_b, gn_eps,
+                       (const bf16_t*)A_log, h, (int)ds, (bf16_t*)out, out_row_stride, (int)y_col,
+                       (int)g_col);
+  return hdcm_launch_status();
+}
+
+extern "C" int hdcm_chunk_pos_advance(int32_t* pos_dev, int64_t C, void* stream) {
+  HDCM_CHECK_ARG(pos_dev != nullptr && C > 0 && C < ((int64_t)1 << 24), HDCM_EINVAL);
+  hipLaunchKernelGGL(chunk_pos_advance_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, (int*)pos_dev,
+                     (int)C);
+  return hdcm_launch_status();
+}

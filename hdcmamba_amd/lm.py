@@ -9,13 +9,15 @@ train_fineweb.py:49-84 so seeded construction draws the same weights.
 """
 from __future__ import annotations
 
+import copy
+
 import torch
 import torch.nn as nn
 
 from . import _ops
-from .model import HdcMamba9v3Model
+from .model import BlockState, HdcMamba9v3Model
 
-__all__ = ["HdcMambaLM", "SIZES"]
+__all__ = ["HdcMambaLM", "DecodeGraph", "SIZES"]
 
 # HdcMamba rows of the reference size table (train_fineweb.py:29-45).
 SIZES = {
@@ -59,3 +61,83 @@ class HdcMambaLM(nn.Module):
         x = self.backbone(x)
         x = _ops.layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
         return self.lm_head(x)
+
+    def _logits(self, x):
+        x = _ops.layer_norm(x.contiguous(), self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
+        return self.lm_head(x)
+
+    def prefill(self, input_ids, last=1):
+        """Forward over input_ids [B,L] returning the logits of the last ``last`` positions
+        ([B,last,V]) and the per-block states for ``step``."""
+        _ops._on_gpu(input_ids)
+        with torch.no_grad():
+            y, states = self.backbone.prefill(self.embedding(input_ids))
+            return self._logits(y[:, y.shape[1] - last:]), states
+
+    def step(self, input_ids, states, pos_dev=None):
+        """One token per batch row: input_ids [B] -> logits [B,V]; states advance in place."""
+        _ops._on_gpu(input_ids)
+        with torch.no_grad():
+            return self._logits(self.backbone.step(self.embedding(input_ids), states, pos_dev))
+
+    def capture_decode(self, states):
+        """A DecodeGraph stepping ``states`` (as returned by prefill) from replays."""
+        return DecodeGraph(self, states)
+
+
+def _clone_state(st):
+    return BlockState(conv=st.conv.clone(), h=st.h.clone(), S_prev=st.S_prev.clone(),
+                      S_intra=st.S_intra.clone(), pos=st.pos)
+
+
+class DecodeGraph:
+    """One decode step of an HdcMambaLM recorded once as a HIP graph and replayed per token.
+
+    The graph reads token ids from a static buffer, runs embedding -> every block's step ->
+    norm_final -> norm_f -> lm_head into a static logits buffer, and advances a device-side
+    chunk offset that every block's mixer step reads, so one recording serves every
+    position.  A replay submits the whole step (about ten kernels per block) at once
+    instead of launching each from Python.  The states passed in are the ones the replays
+    update; ``step`` keeps their host-side ``pos`` in sync.  Replays of one DecodeGraph must
+    not overlap with other work on the same states.
+    """
+
+    def __init__(self, lm, states):
+        chunks = {layer.chunk_size for layer in lm.backbone.layers}
+        pos = {st.pos for st in states}
+        if len(chunks) != 1 or len(pos) != 1 or len(states) != len(lm.backbone.layers):
+            raise RuntimeError("capture_decode needs one chunk size and states at one position")
+        (self.chunk,) = chunks
+        self.lm, self.states = lm, states
+        dev = states[0].h.device
+        B = states[0].h.shape[0]
+        self.ids = torch.zeros(B, dtype=torch.long, device=dev)
+        self.pos = torch.full((1,), states[0].pos, dtype=torch.int32, device=dev)
+        # warm up on scratch copies (library handles, allocator pools), then record
+        scratch = [_clone_state(st) for st in states]
+        scratch_pos = self.pos.clone()
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._run(scratch, scratch_pos)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        del scratch, scratch_pos
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self._run(self.states, self.pos)
+
+    def _run(self, states, pos):
+        with torch.no_grad():
+            logits = self.lm.step(self.ids, states, pos_dev=pos)
+            _ops.chunk_pos_advance(pos, self.chunk)
+        return logits
+
+    def step(self, input_ids):
+        """input_ids [B] -> logits [B,V] (a static buffer, overwritten by the next step)."""
+        self.ids.copy_(input_ids)
+        self.graph.replay()
+        for st in self.states:
+            st.pos = (st.pos + 1) % self.chunk
+        return self.logits

@@ -15,6 +15,8 @@ defects that are not reproduced).  Only GPU tensors are accepted; there is no CP
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -22,7 +24,25 @@ import torch.nn.functional as F
 from . import _ops
 
 __all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
-           "fused_norm_conv1d_trainable"]
+           "fused_norm_conv1d_trainable", "BlockState"]
+
+
+@dataclass
+class BlockState:
+    """What one block carries from a prefill into single-token steps.
+
+    conv     [B,3,dm]     block-input rows t-3..t-1 (activation dtype; zero rows before the
+                          sequence start, whose LayerNorm is the LayerNorm bias)
+    h        [B,ds]       SSM state, fp32
+    S_prev   [B,H,hd,hd]  slot state at the last chunk boundary, fp32
+    S_intra  [B,H,hd,hd]  slot state of the current chunk's tokens, fp32
+    pos                   offset of the next token inside its chunk
+    """
+    conv: torch.Tensor
+    h: torch.Tensor
+    S_prev: torch.Tensor
+    S_intra: torch.Tensor
+    pos: int = 0
 
 
 class FusedNormConv1dFunction(torch.autograd.Function):
@@ -85,39 +105,92 @@ class HdcMamba9v3Block(nn.Module):
         self.group_norm = nn.GroupNorm(num_heads, d_model)
         self.register_buffer("gamma_buf", torch.exp(-F.softplus(self.decay_log)))
 
-    def _mixer(self, x):
+    def _mixer(self, x, state=None):
         """LN+conv, in_proj, SSM and slot+gate into one `combined` row buffer, then its
-        LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm]."""
+        LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm].  With ``state``,
+        the SSM and slot states after the last row are written into it."""
         B, L, dm = x.shape
         ds, H, C = self.d_state, self.num_heads, self.chunk_size
         dtype = x.dtype
         x_conv = fused_norm_conv1d_trainable(x, self.norm, self.conv1d)
         projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
         combined = torch.empty(B, L, ds + dm, device=x.device, dtype=dtype)
-        _ops.ssm(projs, self.A_log, ds, combined[..., :ds])
+        _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h)
         gamma = self.gamma_buf.to(dtype)
         q_col = 3 * ds
         ws = _ops.slot_workspace(projs, dm, H, C)
         _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
-                       combined, ds, dm, H, C)
+                       combined, ds, dm, H, C, S_final=None if state is None else state.S_prev)
         _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
 
-    def _inner_forward(self, x):
+    def _inner_forward(self, x, state=None):
         """Block body on a chunk-aligned [B,L,dm] input; returns x + out_proj(LN(combined))."""
         B, L, dm = x.shape
-        c = self._mixer(x)
+        c = self._mixer(x, state)
         out = torch.addmm(x.reshape(B * L, dm), c, self.out_proj.weight.to(x.dtype).t())
         return out.view(B, L, dm)
 
-    def _residual_step_(self, r):
+    def _residual_step_(self, r, state=None):
         """In-place variant for a model-owned residual stream r [B,L,dm] (chunk-aligned):
         r += out_proj(LN(combined)), with the GEMM accumulating straight into r."""
         B, L, dm = r.shape
-        c = self._mixer(r)
+        if state is not None:
+            self._capture_conv(r, state)
+        c = self._mixer(r, state)
         r.view(B * L, dm).addmm_(c, self.out_proj.weight.to(r.dtype).t())
         return r
+
+    # ------------------------------------------------------------------ prefill / decode
+    def new_state(self, batch, device, dtype):
+        """The state before any token (what a prefill of an empty sequence leaves)."""
+        dm, ds, H, hd = self.d_model, self.d_state, self.num_heads, self.head_dim
+        return BlockState(conv=torch.zeros(batch, 3, dm, device=device, dtype=dtype),
+                          h=torch.zeros(batch, ds, device=device),
+                          S_prev=torch.zeros(batch, H, hd, hd, device=device),
+                          S_intra=torch.zeros(batch, H, hd, hd, device=device), pos=0)
+
+    @staticmethod
+    def _capture_conv(xp, state):
+        n = min(3, xp.shape[1])
+        state.conv.zero_()
+        state.conv[:, 3 - n:].copy_(xp[:, xp.shape[1] - n:])
+        state.S_intra.zero_()
+        state.pos = 0
+
+    def prefill(self, x):
+        """Forward over x [B,L,dm] that also returns the BlockState after its last token.
+        The padded length is a multiple of the chunk, so the next token starts a chunk."""
+        _ops._on_gpu(x)
+        B, L_in, _ = x.shape
+        pad = (self.chunk_size - (L_in % self.chunk_size)) % self.chunk_size
+        xp = F.pad(x, (0, 0, pad, 0)).contiguous() if pad else x.contiguous()
+        state = self.new_state(B, x.device, x.dtype)
+        self._capture_conv(xp, state)
+        y = self._inner_forward(xp, state)
+        return y[:, pad:, :], state
+
+    def step(self, x, state, pos_dev=None):
+        """One token per batch row: x [B,dm] -> y [B,dm]; ``state`` advances in place.
+        With ``pos_dev`` (int32 device scalar) the chunk offset is read on the device and
+        state.pos is left to the caller (graph replay)."""
+        _ops._on_gpu(x)
+        dm, ds, H, C = self.d_model, self.d_state, self.num_heads, self.chunk_size
+        B = x.shape[0]
+        dtype = x.dtype
+        xc = _ops.norm_conv_step(x, self.norm.weight, self.norm.bias, self.conv1d.weight.squeeze(1),
+                                 self.conv1d.bias, self.norm.eps, state.conv)
+        projs = F.linear(xc, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
+        combined = torch.empty(B, ds + dm, device=x.device, dtype=dtype)
+        _ops.mixer_step(projs, self.A_log, ds, 3 * ds, self.gamma_buf.to(dtype), self.group_norm.weight,
+                        self.group_norm.bias, 1e-5, state.h, state.S_prev, state.S_intra, state.pos, C,
+                        combined, dm, H, pos_dev=pos_dev)
+        _ops.layer_norm(combined, eps=1e-5, out=combined)
+        y = torch.addmm(x, combined, self.out_proj.weight.to(dtype).t())
+        if pos_dev is None:
+            state.pos = (state.pos + 1) % C
+        return y
 
     def forward(self, x):
         _ops._on_gpu(x)
@@ -168,3 +241,33 @@ class HdcMamba9v3Model(nn.Module):
             x = r[:, pad:]
         return _ops.layer_norm(x.contiguous(), self.norm_final.weight, self.norm_final.bias,
                                self.norm_final.eps)
+
+    def prefill(self, x):
+        """Forward over x [B,L,dm] (inference) that also returns every block's BlockState."""
+        _ops._on_gpu(x)
+        chunks = {layer.chunk_size for layer in self.layers}
+        if len(chunks) != 1:
+            raise RuntimeError("prefill needs one chunk size for all blocks")
+        (C,) = chunks
+        B, L, dm = x.shape
+        pad = (C - L % C) % C
+        r = torch.empty(B, L + pad, dm, device=x.device, dtype=x.dtype)
+        r[:, pad:].copy_(x)
+        states = []
+        with torch.no_grad():
+            for layer in self.layers:
+                if pad:
+                    r[:, :pad].zero_()
+                st = layer.new_state(B, x.device, x.dtype)
+                layer._residual_step_(r, st)
+                states.append(st)
+        y = _ops.layer_norm(r[:, pad:].contiguous(), self.norm_final.weight, self.norm_final.bias,
+                            self.norm_final.eps)
+        return y, states
+
+    def step(self, x, states, pos_dev=None):
+        """One token per batch row through every block and norm_final: x [B,dm] -> [B,dm]."""
+        with torch.no_grad():
+            for layer, st in zip(self.layers, states):
+                x = layer.step(x, st, pos_dev)
+        return _ops.layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)

@@ -108,6 +108,42 @@ int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col
                        int64_t H, int64_t C, int dtype, void* stream);
 
 /*
+ * Recurrent decode (one token per batch row) after a prefill.  No counterpart in the
+ * reference, whose only generation path re-runs the whole forward
+ * (hdcmamba/train.py:139-151); the semantics are those of the chunked forward continued
+ * token by token (hdcmamba/model.py:22-72, 175-233, 236-295).
+ *
+ * hdcm_norm_conv_step_fwd: LayerNorm + causal width-4 conv of x[b,:] (row stride
+ * x_row_stride) using hist [B,3,D] (activation dtype, contiguous), the raw block-input
+ * rows t-3, t-2, t-1 (zero rows before the sequence start, whose LayerNorm is ln_b).
+ * Writes out[b,:] and shifts x into hist.  Same weights as hdcm_norm_conv_fwd; needs
+ * D % (16/elt_size) == 0 and D/(16/elt_size) <= 1024.
+ *
+ * hdcm_mixer_step_fwd: one token of the SSM (h [B,ds] fp32, updated) and of the slot
+ * memory + GroupNorm + gate, reading one projs row per batch row (columns as in
+ * hdcm_ssm_fwd at 0 and hdcm_slot_state_fwd at q_col).  The slot state is the pair
+ * S_prev [B,H,hd,hd] (chunk-boundary state, as hdcm_slot_gate_fwd's S_final) and
+ * S_intra [B,H,hd,hd] (this chunk's tokens so far; zero at a chunk start), both fp32 and
+ * updated; pos = t mod C is the token's offset in its chunk (0 right after a prefill,
+ * whose padded length is a multiple of C).  Writes y_ssm to columns [y_col, y_col+ds) and
+ * the gated slot output to [g_col, g_col+dm) of out.  Needs hd <= 128.  With pos_dev
+ * non-NULL the offset is read from that device int32 instead of pos, so one captured
+ * graph of a decode step serves every position; hdcm_chunk_pos_advance then moves it to
+ * (pos + 1) mod C on the stream (no counterpart in the reference: graph replay support).
+ */
+int hdcm_norm_conv_step_fwd(const void* x, int64_t x_row_stride, const void* ln_w,
+                            const void* ln_b, const void* conv_w, const void* conv_b, void* hist,
+                            void* out, int64_t out_row_stride, int64_t B, int64_t D, float eps,
+                            int dtype, void* stream);
+int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col,
+                        const void* A_log, float* h, const void* gamma, float* S_prev,
+                        float* S_intra, int64_t pos, const int32_t* pos_dev, int64_t C,
+                        const void* gn_w, const void* gn_b, float gn_eps, void* out,
+                        int64_t out_row_stride, int64_t y_col, int64_t g_col, int64_t B,
+                        int64_t dm, int64_t ds, int64_t H, int dtype, void* stream);
+int hdcm_chunk_pos_advance(int32_t* pos_dev, int64_t C, void* stream);
+
+/*
  * Row LayerNorm over `width` columns, fp32 statistics, optional affine
  * (w, b may be NULL).  in and out may be the same buffer.
  * Replaces: F.layer_norm(combined.float(), (ds+dm,)).to(dtype)

@@ -32,6 +32,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle_*.py):
 * ``slot_chunked``   -- pinned: equals ``slot_sequential`` (fp32) for several chunk sizes.
 * ``gnorm_gate``     -- pinned: F.group_norm per token + torch.sigmoid.
 * ``rowln``          -- pinned: F.layer_norm.
+* ``block_forward_stream`` -- pinned: equals ``block_forward`` when the whole sequence is
+  the prefill, and row by row equals a sequential recurrence over the padded sequence
+  (every stage is causal, so right padding changes no kept row).
 * faithful-mode address maps (B1-B3, B5) -- pinned only by hand-computed index
   KATs restated from the launch arguments; parity with the reference's GPU
   execution is unpinned (the reference needs a CUDA GPU and Triton).
@@ -47,7 +50,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "BlockCfg", "kernel_rounding", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
-    "slot_sequential", "slot_chunked", "gnorm_gate", "rowln", "block_forward",
+    "slot_sequential", "slot_chunked", "gnorm_gate", "rowln", "block_forward", "block_forward_stream",
     "model_forward", "lm_forward", "init_block_params",
 ]
 
@@ -359,16 +362,33 @@ def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_st
     """One HdcMamba9v3Block forward in eval mode (model.py:386-394 + 331-384).
 
     ``p`` is the block's state_dict (tensors in the model dtype); ``x`` is [B,L,D].
+    L is left-padded with zero rows to a multiple of the chunk (model.py:388-389).
     """
+    C = cfg.chunk_size
+    pad = (C - x.shape[1] % C) % C
+    return _block_padded(p, x, cfg, pad, 0, semantics, eps, return_states)
+
+
+def block_forward_stream(p, x, cfg: BlockCfg, n_prefill, eps=1e-5):
+    """A prefill of x[:, :n_prefill] continued token by token over the remaining rows
+    (intended semantics): the chunk grid is the prefill's (left pad to a multiple of C),
+    and the sequence is right-padded to a whole chunk.  Every stage is causal, so the
+    right padding changes no kept row.  Returns [B,L,D]."""
+    C = cfg.chunk_size
+    pad_l = (C - n_prefill % C) % C
+    pad_r = (C - (pad_l + x.shape[1]) % C) % C
+    return _block_padded(p, x, cfg, pad_l, pad_r, "intended", eps, False)
+
+
+def _block_padded(p, x, cfg, pad, pad_r, semantics, eps, return_states):
     dtype = x.dtype
     dm, ds, H, C = cfg.d_model, cfg.d_state, cfg.num_heads, cfg.chunk_size
     hd = cfg.head_dim
     if semantics == "faithful" and C > 128:
         raise ValueError("faithful semantics undefined for chunk_size > 128 (model.py:17,245-246)")
     B, L_in, _ = x.shape
-    pad = (C - L_in % C) % C
-    if pad:
-        x = F.pad(x, (0, 0, pad, 0))
+    if pad or pad_r:
+        x = F.pad(x, (0, 0, pad, pad_r))
     L = x.shape[1]
     x_conv = norm_conv(x, p["norm.weight"], p["norm.bias"], p["conv1d.weight"].squeeze(1),
                        p["conv1d.bias"], eps)
@@ -392,7 +412,7 @@ def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_st
     combined = torch.cat([_rnd(y_ssm_t, dtype), _rnd(g, dtype)], -1).to(dtype)
     c = F.layer_norm(combined.float(), (ds + dm,)).to(dtype)
     res = F.linear(c, p["out_proj.weight"].to(dtype))
-    out = (x + res)[:, pad:, :]
+    out = (x + res)[:, pad:pad + L_in, :]
     if return_states:
         return out, {"h": h_fin, "S": s_fin, "projs": projs, "combined": combined, "x_conv": x_conv}
     return out
@@ -403,18 +423,21 @@ def _sub(sd, prefix):
     return {k[n:]: v for k, v in sd.items() if k.startswith(prefix)}
 
 
-def model_forward(sd, x, cfg: BlockCfg, n_layers, semantics="intended", layers=None):
-    """HdcMamba9v3Model.forward (model.py:402-404): blocks then norm_final."""
+def model_forward(sd, x, cfg: BlockCfg, n_layers, semantics="intended", layers=None, n_prefill=None):
+    """HdcMamba9v3Model.forward (model.py:402-404): blocks then norm_final.  With
+    ``n_prefill``, the blocks run as a prefill of that many rows continued token by token
+    (block_forward_stream)."""
     for i in (range(n_layers) if layers is None else layers):
-        x = block_forward(_sub(sd, f"layers.{i}."), x, cfg, semantics)
+        p = _sub(sd, f"layers.{i}.")
+        x = block_forward(p, x, cfg, semantics) if n_prefill is None else block_forward_stream(p, x, cfg, n_prefill)
     return F.layer_norm(x, (cfg.d_model,), sd["norm_final.weight"], sd["norm_final.bias"], 1e-5)
 
 
-def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None):
+def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None, n_prefill=None):
     """UniversalLM.forward, HdcMamba arm (train_fineweb.py:86-94): embedding, backbone,
-    norm_f, tied lm_head."""
+    norm_f, tied lm_head.  ``n_prefill`` as in model_forward."""
     x = F.embedding(ids, sd["embedding.weight"])
-    x = model_forward(_sub(sd, "backbone."), x, cfg, n_layers, semantics, layers)
+    x = model_forward(_sub(sd, "backbone."), x, cfg, n_layers, semantics, layers, n_prefill)
     x = F.layer_norm(x, (cfg.d_model,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)
     return F.linear(x, sd["embedding.weight"])
 

@@ -20,6 +20,9 @@ WORKLOADS = {
                   dtype=torch.bfloat16),
     "lm_c4": dict(d_model=1024, d_state=128, num_heads=16, chunk=64, n_layers=24, B=1, L=32768,
                   dtype=torch.bfloat16),
+    # prefill B=16 x 8192, then 256 single-token decode steps
+    "lm_c5": dict(d_model=2048, d_state=128, num_heads=32, chunk=64, n_layers=48, B=16, L=8192,
+                  decode_steps=256, dtype=torch.bfloat16),
 }
 
 

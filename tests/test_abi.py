@@ -100,6 +100,40 @@ def test_slot_validation():
     assert g(*a) == EINVAL
 
 
+def test_decode_step_validation():
+    lib = _ops.lib()
+    # hdcm_norm_conv_step_fwd(x, x_rs, ln_w, ln_b, conv_w, conv_b, hist, out, out_rs, B, D, eps, dtype, stream)
+    f = lib.hdcm_norm_conv_step_fwd
+    base = [P16, 256, P16, P16, P16, P16, P16, P16, 256, 4, 256, 1e-5, 1, None]
+    a = list(base); a[6] = None  # no history buffer
+    assert f(*a) == EINVAL
+    a = list(base); a[10] = 250  # D not whole 16-byte groups
+    a[1] = a[8] = 250
+    assert f(*a) == EALIGN
+    a = list(base); a[10] = a[1] = a[8] = 8 * 4 * 256 + 8  # wider than the kernel's row tiling
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[9] = 0
+    assert f(*a) == OK
+    # hdcm_mixer_step_fwd(projs, prs, q_col, A_log, h, gamma, S_prev, S_intra, pos, C, gn_w, gn_b, eps,
+    #                     out, ors, y_col, g_col, B, dm, ds, H, dtype, stream)
+    g = lib.hdcm_mixer_step_fwd
+    P = 3 * 64 + 4 * 256
+    gb = [P16, P, 3 * 64, P16, P16, P16, P16, P16, 0, None, 64, P16, P16, 1e-5, P16, 64 + 256, 0, 64, 4, 256,
+          64, 4, 1, None]
+    a = list(gb); a[8] = 64  # pos must be inside the chunk
+    assert g(*a) == EINVAL
+    a = list(gb); a[7] = None  # S_intra
+    assert g(*a) == EINVAL
+    a = list(gb); a[19] = 1040; a[21] = 4; a[1] = 3 * 64 + 4 * 1040  # head dim 260
+    a[15] = 64 + 1040
+    assert g(*a) == EUNSUPPORTED
+    a = list(gb); a[15] = 200  # output row too short
+    assert g(*a) == EINVAL
+    a = list(gb); a[18] = 0
+    assert g(*a) == OK
+    assert lib.hdcm_chunk_pos_advance(None, 64, None) == EINVAL
+
+
 def test_rowln_validation():
     f = _ops.lib().hdcm_rowln_fwd
     base = [P16, 1152, P16, 1152, None, None, 10, 1152, 1e-5, 1, None]
