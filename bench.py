@@ -220,6 +220,9 @@ def main():
                          "single-token decode steps (a separate measurement, not the headline line)")
     ap.add_argument("--eager", action="store_true", help="lm_c5_decode: step from Python instead of "
                     "replaying the captured decode graph")
+    ap.add_argument("--graph", default="on", choices=["on", "off"],
+                    help="LM workloads: time replays of the forward recorded as a HIP graph "
+                         "(on) or eager forwards (off)")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -262,21 +265,34 @@ def main():
         workload = f"one HdcMamba block forward, B={cfg['B']}, L={cfg['L']}, d_model={cfg['d_model']}"
     tokens = cfg["B"] * cfg["L"]
 
+    use_graph = args.graph == "on" and args.workload.startswith("lm")
     with torch.no_grad():
+        runner = model.capture_forward(inp) if use_graph else model
         for _ in range(args.warmup):
-            model(inp)
+            runner(inp)
         torch.cuda.synchronize()
-        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln"}
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            model(inp)
+            runner(inp)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
+        # Per-kernel durations: HIP events on the launch stream around every custom kernel,
+        # over eager forwards (launches inside a graph replay cannot be bracketed).
+        k_steps = max(1, min(args.steps, 5))
+        model(inp)
+        torch.cuda.synchronize()
+        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln"}
+        t2 = time.perf_counter()
+        for _ in range(k_steps):
+            model(inp)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
         _ops.timer.active = set()
     times = _ops.timer.collect()
     sec = t1 - t0
     ms_per_step = sec / args.steps * 1e3
     value = tokens * args.steps / sec
+    eager_ms = (t3 - t2) / k_steps * 1e3
 
     kernels = {}
     for name, ms in times.items():
@@ -312,6 +328,9 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "timing": {"steps": "HIP graph replays of the whole forward" if use_graph else "eager forwards",
+                   "kernels": f"HIP events around each custom kernel over {k_steps} eager forwards",
+                   "eager_ms_per_step": round(eager_ms, 3)},
         "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)

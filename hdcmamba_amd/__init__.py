@@ -9,7 +9,7 @@ from .model import (
     HdcMamba9v3Model,
     fused_norm_conv1d_trainable,
 )
-from .lm import DecodeGraph, HdcMambaLM
+from .lm import DecodeGraph, ForwardGraph, HdcMambaLM
 
 __all__ = [
     "HdcMamba9v3Block",
@@ -19,4 +19,5 @@ __all__ = [
     "HdcMambaLM",
     "BlockState",
     "DecodeGraph",
+    "ForwardGraph",
 ]

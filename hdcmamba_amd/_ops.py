@@ -95,6 +95,21 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_side_streams = {}
+
+
+def side_stream(device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for work that can overlap the
+    current stream's kernels; callers fork and join it with wait_stream."""
+    idx = torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    s = _side_streams.get(idx)
+    if s is None:
+        s = _side_streams[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
 def _same(t: torch.Tensor, ref: torch.Tensor, name: str) -> torch.Tensor:
     if t.dtype != ref.dtype:
         t = t.to(ref.dtype)

@@ -17,7 +17,7 @@ import torch.nn as nn
 from . import _ops
 from .model import BlockState, HdcMamba9v3Model
 
-__all__ = ["HdcMambaLM", "DecodeGraph", "SIZES"]
+__all__ = ["HdcMambaLM", "DecodeGraph", "ForwardGraph", "SIZES"]
 
 # HdcMamba rows of the reference size table (train_fineweb.py:29-45).
 SIZES = {
@@ -84,6 +84,10 @@ class HdcMambaLM(nn.Module):
         """A DecodeGraph stepping ``states`` (as returned by prefill) from replays."""
         return DecodeGraph(self, states)
 
+    def capture_forward(self, input_ids):
+        """A ForwardGraph replaying this model's inference forward at input_ids' shape."""
+        return ForwardGraph(self, input_ids)
+
 
 def _clone_state(st):
     return BlockState(conv=st.conv.clone(), h=st.h.clone(), S_prev=st.S_prev.clone(),
@@ -141,3 +145,46 @@ class DecodeGraph:
         for st in self.states:
             st.pos = (st.pos + 1) % self.chunk
         return self.logits
+
+
+class ForwardGraph:
+    """The inference forward of an HdcMambaLM at one input shape, recorded once as a HIP
+    graph and replayed per call.
+
+    A forward at B=1, L=32768 issues about 245 kernels (ten per block); launched one by
+    one from Python they leave the GPU idle between launches for about 7% of the forward.
+    A replay submits the recorded sequence at once, including the side-stream fork and
+    join of every block.  ``forward(input_ids)`` copies the ids into the static input
+    buffer and returns the static logits buffer, which the next replay overwrites.  The
+    weights are read at replay time (in place updates are seen); the recorded shapes,
+    dtypes and buffers are fixed.
+    """
+
+    def __init__(self, lm, input_ids, warmup=2):
+        _ops._on_gpu(input_ids)
+        if lm.training:
+            raise RuntimeError("capture_forward records the inference forward; call eval() first")
+        dev = input_ids.device
+        self.lm = lm
+        self.ids = input_ids.detach().clone()
+        # warm library handles and allocator pools outside the recording
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(warmup):
+                lm(self.ids)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.no_grad(), torch.cuda.graph(self.graph):
+            self.logits = lm(self.ids)
+
+    def forward(self, input_ids):
+        if input_ids.shape != self.ids.shape:
+            raise RuntimeError(f"ForwardGraph was recorded for ids of shape {tuple(self.ids.shape)}, "
+                               f"got {tuple(input_ids.shape)}")
+        self.ids.copy_(input_ids)
+        self.graph.replay()
+        return self.logits
+
+    __call__ = forward

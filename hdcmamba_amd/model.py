@@ -115,13 +115,22 @@ class HdcMamba9v3Block(nn.Module):
         x_conv = fused_norm_conv1d_trainable(x, self.norm, self.conv1d)
         projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
         combined = torch.empty(B, L, ds + dm, device=x.device, dtype=dtype)
-        _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h)
+        # The SSM (latency-bound: three short launches) and the slot kernels read projs
+        # and write disjoint columns of `combined`, so the SSM runs on a side stream and
+        # overlaps the slot passes.  The join below orders every later use (and the
+        # allocator's reuse) of projs and combined after it.
+        main = torch.cuda.current_stream(x.device)
+        side = _ops.side_stream(x.device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h)
         gamma = self.gamma_buf.to(dtype)
         q_col = 3 * ds
         ws = _ops.slot_workspace(projs, dm, H, C)
         _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
                        combined, ds, dm, H, C, S_final=None if state is None else state.S_prev)
+        main.wait_stream(side)
         _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
 

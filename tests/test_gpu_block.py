@@ -88,3 +88,29 @@ def test_model_inplace_stream(dev, L):
     with torch.no_grad():
         y = m.to(dev)(x.to(dev))
     assert_close(y, ref, torch.float32, f"model L={L}")
+
+
+def test_forward_graph_replays_match_eager(dev):
+    """Every replay of a recorded LM forward (padded length, side-stream fork/join in every
+    block) equals the eager forward on the same ids; eager work and synchronisations run
+    between the replays, and a replay after a weight update in place sees the new weight."""
+    print("forward graph", flush=True)
+    lm = make_lm("lm_c3", n_layers=2).to(torch.bfloat16).to(dev)
+    ids = [lm_input("lm_c3", B=2, L=200, seed=s).to(dev) for s in (1, 2, 3)]
+    with torch.no_grad():
+        fg = lm.capture_forward(ids[0])
+        for rep in range(6):
+            x = ids[rep % 3]
+            want = lm(x)
+            torch.cuda.synchronize()
+            got = fg(x).clone()
+            torch.cuda.synchronize()
+            err = max_rel(got, want)
+            print("  replay", rep, "max rel vs eager", err, flush=True)
+            assert err < 1e-3, f"replay {rep}: {err}"
+        lm.backbone.layers[1].out_proj.weight.mul_(0.5)
+        want = lm(ids[0])
+        got = fg(ids[0]).clone()
+        assert max_rel(got, want) < 1e-3
+    with pytest.raises(RuntimeError):
+        fg(ids[0][:, :100])
