@@ -67,12 +67,21 @@ template <typename T> __device__ __forceinline__ void store16(T* p, const float*
 template <> __device__ __forceinline__ void store16<float>(float* p, const float* in) {
   *reinterpret_cast<float4*>(p) = make_float4(in[0], in[1], in[2], in[3]);
 }
+// Two fp32 values rounded (nearest even) into one packed bf16 pair: a single
+// v_cvt_pk_bf16_f32 with both sources.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, b16x2));
+}
+
 template <> __device__ __forceinline__ void store16<bf16_t>(bf16_t* p, const float* in) {
   uint4 v;
-  v.x = (uint32_t)f2bf(in[0]) | ((uint32_t)f2bf(in[1]) << 16);
-  v.y = (uint32_t)f2bf(in[2]) | ((uint32_t)f2bf(in[3]) << 16);
-  v.z = (uint32_t)f2bf(in[4]) | ((uint32_t)f2bf(in[5]) << 16);
-  v.w = (uint32_t)f2bf(in[6]) | ((uint32_t)f2bf(in[7]) << 16);
+  v.x = pack_bf16x2(in[0], in[1]);
+  v.y = pack_bf16x2(in[2], in[3]);
+  v.z = pack_bf16x2(in[4], in[5]);
+  v.w = pack_bf16x2(in[6], in[7]);
   *reinterpret_cast<uint4*>(p) = v;
 }
 
@@ -99,6 +108,18 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
+}
+
+// Sum over all 64 lanes on DPP lane moves (quad swaps, half-row and row mirrors, then
+// row_bcast 15/31 fold the rows into lane 63), read into a wave-uniform scalar.
+__device__ __forceinline__ float wave_total(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));  // row_mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Sum over the four lanes l, l^16, l^32, l^48 (the row groups of an MFMA C/D tile).

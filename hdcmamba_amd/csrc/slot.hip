@@ -350,6 +350,22 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   uint4 raw[TL::NL];
   loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
 
+  // Gate values of this lane's output positions (row 16*w + l16 of a tile, columns
+  // 16*vt + 4*kg .. +3), kept as stored.  They are loaded one tile ahead, right after the
+  // current tile's outputs, so the load overlaps the state update, the next tile's
+  // staging and both barriers.  Rows past the tile read the tile's first row (never
+  // stored), which keeps the load count fixed and the memory-counter waits exact.
+  typedef typename std::conditional<sizeof(T) == 2, uint2, float4>::type G4;
+  G4 graw[NVT];
+  const int giq = (w < NIT ? w : 0) * 16 + l16;
+  auto load_gate = [&](int pt) {
+    const int tl = min(TC, L - pt);
+    const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * prs + kg * 4;
+#pragma unroll
+    for (int vt = 0; vt < NVT; ++vt) graw[vt] = *reinterpret_cast<const G4*>(grow + vt * 16);
+  };
+  if (w < NIT) load_gate(p_begin);
+
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
     __syncthreads();
@@ -388,14 +404,6 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     if (w < NIT) {
       const int it = w;
       const int iq = it * 16 + l16;
-      // gate values of this lane's output positions, loaded early and kept as stored
-      typedef typename std::conditional<sizeof(T) == 2, uint2, float4>::type G4;
-      G4 graw[NVT];
-      if (iq < tlen) {
-        const T* grow = gatebase + (rowbase + p + iq) * prs + kg * 4;
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) graw[vt] = *reinterpret_cast<const G4*>(grow + vt * 16);
-      }
       f32x4_t yacc[NVT];
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt) yacc[vt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -490,6 +498,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           store4<T>(orow + vt * 16, o);
         }
       }
+      // next tile's gate (this tile's again after the last: a fixed load count)
+      load_gate(p + TC < p_end ? p + TC : p);
     }
 
     // ---- state update: (W or A) <- gamma^tlen * (W or A) + K~^T V
