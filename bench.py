@@ -223,6 +223,9 @@ def main():
     ap.add_argument("--graph", default="on", choices=["on", "off"],
                     help="LM workloads: time replays of the forward recorded as a HIP graph "
                          "(on) or eager forwards (off)")
+    ap.add_argument("--tuned-gemms", default="on", choices=["on", "off"],
+                    help="run in_proj/out_proj/LM head on the hipBLASLt/rocBLAS solutions recorded "
+                         "in hdcmamba_amd/tuned/gemm_gfx950.csv (TunableOp, tuning off)")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -248,6 +251,9 @@ def main():
 
     from cfgs import WORKLOADS, block_input, lm_input, make_block, make_lm
     from hdcmamba_amd import _ops
+    from hdcmamba_amd.gemm_tuning import use_tuned_gemms
+
+    n_tuned = use_tuned_gemms() if args.tuned_gemms == "on" else 0
 
     dev = torch.device("cuda:0")
     if args.workload == "lm_c5_decode":
@@ -331,6 +337,8 @@ def main():
         "timing": {"steps": "HIP graph replays of the whole forward" if use_graph else "eager forwards",
                    "kernels": f"HIP events around each custom kernel over {k_steps} eager forwards",
                    "eager_ms_per_step": round(eager_ms, 3)},
+        "gemm_solutions": (f"TunableOp file, {n_tuned} recorded GEMM signatures" if n_tuned
+                           else "library default heuristics"),
         "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)

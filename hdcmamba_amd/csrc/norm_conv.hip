@@ -9,17 +9,13 @@
 // per lane and the three history rows stay in registers.  The LN affine is folded into
 // the taps:  out = sum_k (w*c_k) * xhat[t-3+k] + (b*sum_k c_k + c_b), xhat = (x-mu)*rstd,
 // which makes the t<0 halo exactly xhat = 0.  Raw rows are prefetched PF rows ahead so
-// several 128-bit loads per lane are in flight while the current row is reduced.
+// several 128-bit loads per lane are in flight while the current row is reduced.  The two
+// row reductions run on DPP lane moves and end in a scalar register (wave_total).
 //
-// When half a row fills a wave (D/2 >= 64 16-byte groups, e.g. bf16 D = 1024 or 2048),
-// norm_conv_split_kernel is used instead: a workgroup of two waves walks kSplitRows rows,
-// wave w owning columns [w*D/2, (w+1)*D/2).  Each wave reduces its half-row on DPP lane
-// moves into a scalar mean m_w and centred sum of squares M2_w; the halves are merged with
-// Chan's formula (mean = (m_0+m_1)/2, M2 = M2_0 + M2_1 + (m_1-m_0)^2 * D/4) through LDS,
-// one barrier per row.  Halving the columns per lane halves the registers that hold the
-// folded taps and the three history rows, which raises occupancy from 2 to 4 waves per
-// SIMD.  Blocks are numbered so that each XCD walks one contiguous range of rows, which
-// keeps the 3-row halo of a block in the L2 that just read it as its neighbour's tail.
+// Measured alternatives that ran slower inside the model's forward (the preceding
+// out_proj GEMM leaves the residual rows in the caches in its own order): two waves per
+// row with Chan-merged half-row statistics (higher occupancy, one barrier per row), and
+// numbering blocks so that each XCD walks a contiguous range of rows.
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -51,7 +47,7 @@ __device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&xh)[NG][V
 #pragma unroll
     for (int e = 0; e < E; ++e) s += xh[i][e];
   }
-  const float mean = wave_sum(s) * invD;
+  const float mean = wave_total(s) * invD;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NG; ++i) {
@@ -63,7 +59,7 @@ __device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&xh)[NG][V
       q += c * c;
     }
   }
-  const float rstd = rsqrtf(wave_sum(q) * invD + eps);
+  const float rstd = rsqrtf(wave_total(q) * invD + eps);
 #pragma unroll
   for (int i = 0; i < NG; ++i)
 #pragma unroll
@@ -175,172 +171,6 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void norm_conv_kernel(
   }
 }
 
-
-// Block index -> row-run index: XCD x (blocks are dealt to the 8 XCDs round robin) gets the
-// contiguous runs [x*n/8, (x+1)*n/8), so neighbouring runs share an L2.
-__device__ __forceinline__ int64_t xcd_run(int64_t b, int64_t n) {
-  if (n & 7) return b;
-  return (b & 7) * (n >> 3) + (b >> 3);
-}
-
-constexpr int kSplitRows = 32;
-constexpr int kSplitPF = 4;
-
-template <typename T, int NG, bool FULL>
-__global__ __launch_bounds__(2 * kWave) void norm_conv_split_kernel(
-    const T* __restrict__ x, int64_t x_bs, int64_t x_rs, const T* __restrict__ ln_w,
-    const T* __restrict__ ln_b, const T* __restrict__ conv_w, const T* __restrict__ conv_b,
-    T* __restrict__ out, int64_t o_bs, int64_t o_rs, int L, int D, float eps) {
-  constexpr int E = Vec<T>::N;
-  __shared__ float2 sst[2][2];  // [row parity][wave]: (half-row mean, centred sum of squares)
-  const int lane = threadIdx.x & (kWave - 1);
-  const int w = threadIdx.x / kWave;
-  const int64_t t0 = xcd_run(blockIdx.x, gridDim.x) * kSplitRows;
-  const int half = D / 2;
-  const int G = half / E;  // 16-byte groups per half-row
-  const float invHalf = 1.0f / (float)half, invD = 1.0f / (float)D;
-  const float cross = 0.25f * (float)D;  // n_0 n_1 / n for two equal halves
-  const T* xb = x + (int64_t)blockIdx.y * x_bs + w * half;
-  T* ob = out + (int64_t)blockIdx.y * o_bs + w * half;
-
-  float wc[4][NG][E], bt[NG][E];
-#pragma unroll
-  for (int i = 0; i < NG; ++i) {
-    const int g = lane + kWave * i;
-    float lw[E], lb[E], cb[E], cw[4 * E];
-    if (FULL || g < G) {
-      const int c = w * half + g * E;
-      load16<T>(ln_w + c, lw);
-      load16<T>(ln_b + c, lb);
-      load16<T>(conv_b + c, cb);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)c * 4 + k * E, cw + k * E);
-    } else {
-#pragma unroll
-      for (int e = 0; e < E; ++e) { lw[e] = 0.f; lb[e] = 0.f; cb[e] = 0.f; }
-#pragma unroll
-      for (int e = 0; e < 4 * E; ++e) cw[e] = 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float c0 = cw[4 * e + 0], c1 = cw[4 * e + 1], c2 = cw[4 * e + 2], c3 = cw[4 * e + 3];
-      wc[0][i][e] = lw[e] * c0;
-      wc[1][i][e] = lw[e] * c1;
-      wc[2][i][e] = lw[e] * c2;
-      wc[3][i][e] = lw[e] * c3;
-      bt[i][e] = lb[e] * (c0 + c1 + c2 + c3) + cb[e];
-    }
-  }
-
-  int par = 0;
-  // LayerNorm of one row: every call runs in both waves (one barrier each).
-  auto ln = [&](const uint4 (&raw)[NG], float (&h)[NG][E]) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      unpack16<T>(raw[i], h[i]);
-#pragma unroll
-      for (int e = 0; e < E; ++e) s += h[i][e];
-    }
-    const float mw = wave_total(s) * invHalf;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      const bool ok = FULL || (lane + kWave * i) < G;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float c = ok ? h[i][e] - mw : 0.f;
-        q += c * c;
-      }
-    }
-    const float m2 = wave_total(q);
-    if (lane == 0) sst[par][w] = make_float2(mw, m2);
-    __syncthreads();
-    const float2 o = sst[par][w ^ 1];
-    par ^= 1;
-    const float d = o.x - mw;
-    const float mean = 0.5f * (mw + o.x);
-    const float rstd = rsqrtf((m2 + o.y + d * d * cross) * invD + eps);
-#pragma unroll
-    for (int i = 0; i < NG; ++i)
-#pragma unroll
-      for (int e = 0; e < E; ++e) h[i][e] = (h[i][e] - mean) * rstd;
-  };
-
-  uint4 ring[kSplitPF][NG];
-#pragma unroll
-  for (int p = 0; p < kSplitPF; ++p) {
-    const int64_t t = t0 + p < L ? t0 + p : L - 1;
-    load_row<T, NG>(ring[p], xb + t * x_rs, lane, G);
-  }
-  float h3[NG][E], h2[NG][E], h1[NG][E];
-  {
-    uint4 r3[NG], r2[NG], r1[NG];
-    load_row<T, NG>(r3, xb + (t0 >= 3 ? t0 - 3 : 0) * x_rs, lane, G);
-    load_row<T, NG>(r2, xb + (t0 >= 2 ? t0 - 2 : 0) * x_rs, lane, G);
-    load_row<T, NG>(r1, xb + (t0 >= 1 ? t0 - 1 : 0) * x_rs, lane, G);
-    ln(r3, h3);
-    ln(r2, h2);
-    ln(r1, h1);
-    if (t0 < 3) {
-#pragma unroll
-      for (int i = 0; i < NG; ++i)
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-          if (t0 < 3) h3[i][e] = 0.f;
-          if (t0 < 2) h2[i][e] = 0.f;
-          if (t0 < 1) h1[i][e] = 0.f;
-        }
-    }
-  }
-
-#pragma unroll
-  for (int r = 0; r < kSplitRows; ++r) {
-    uint4 cur[NG];
-#pragma unroll
-    for (int i = 0; i < NG; ++i) cur[i] = ring[r % kSplitPF][i];
-    if (r + kSplitPF < kSplitRows) {
-      const int64_t tn = t0 + r + kSplitPF < L ? t0 + r + kSplitPF : L - 1;
-      load_row<T, NG>(ring[r % kSplitPF], xb + tn * x_rs, lane, G);
-    }
-    // both waves run every row (the LayerNorm barrier); rows past L are not stored
-    float h0[NG][E];
-    ln(cur, h0);
-    const int64_t t = t0 + r;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      const int g = lane + kWave * i;
-      float o[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        o[e] = wc[0][i][e] * h3[i][e] + wc[1][i][e] * h2[i][e] + wc[2][i][e] * h1[i][e] +
-               wc[3][i][e] * h0[i][e] + bt[i][e];
-        h3[i][e] = h2[i][e];
-        h2[i][e] = h1[i][e];
-        h1[i][e] = h0[i][e];
-      }
-      if (t < L && (FULL || g < G)) store16<T>(ob + t * o_rs + (int64_t)g * E, o);
-    }
-  }
-}
-
-template <typename T, int NG>
-int launch_split(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const void* ln_b,
-                 const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
-                 int64_t B, int64_t L, int64_t D, float eps, hipStream_t s) {
-  dim3 grid((unsigned)((L + kSplitRows - 1) / kSplitRows), (unsigned)B);
-  const bool full = (D / 2 / Vec<T>::N) == NG * kWave;
-  if (full)
-    hipLaunchKernelGGL((norm_conv_split_kernel<T, NG, true>), grid, dim3(2 * kWave), 0, s, (const T*)x,
-                       x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w, (const T*)conv_b,
-                       (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
-  else
-    hipLaunchKernelGGL((norm_conv_split_kernel<T, NG, false>), grid, dim3(2 * kWave), 0, s, (const T*)x,
-                       x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w, (const T*)conv_b,
-                       (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
-  return hdcm_launch_status();
-}
-
 template <typename T, int NG, int kRows>
 void launch_rows(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const void* ln_b,
                  const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
@@ -352,6 +182,7 @@ void launch_rows(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, co
                      (const T*)conv_b, (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
 }
 
+// 16 rows per wave: the 3-row halo is re-read for every 16 rows.
 template <typename T, int NG>
 int launch_ng(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const void* ln_b,
               const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
@@ -365,14 +196,6 @@ int launch(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, const vo
            const void* conv_w, const void* conv_b, void* out, int64_t o_bs, int64_t o_rs,
            int64_t B, int64_t L, int64_t D, float eps, hipStream_t s) {
   const int G = (int)(D / Vec<T>::N);
-  // two waves per row when each half-row fills a wave with whole 16-byte groups
-  if (D % (2 * Vec<T>::N) == 0 && G / 2 >= kWave) {
-    const int ng2 = (G / 2 + kWave - 1) / kWave;
-    if (ng2 == 1)
-      return launch_split<T, 1>(x, x_bs, x_rs, ln_w, ln_b, conv_w, conv_b, out, o_bs, o_rs, B, L, D, eps, s);
-    if (ng2 == 2)
-      return launch_split<T, 2>(x, x_bs, x_rs, ln_w, ln_b, conv_w, conv_b, out, o_bs, o_rs, B, L, D, eps, s);
-  }
   const int ng = (G + kWave - 1) / kWave;
 #define HDCM_NG_CASE(n) \
   case n:               \

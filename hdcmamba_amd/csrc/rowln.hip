@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
 #pragma unroll
       for (int e = 0; e < E; ++e) s += v[i][e];
     }
-    const float mean = wave_sum(s) * invW;
+    const float mean = wave_total(s) * invW;
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
         q += c * c;
       }
     }
-    const float rstd = rsqrtf(wave_sum(q) * invW + eps);
+    const float rstd = rsqrtf(wave_total(q) * invW + eps);
     if (row < rows) {
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
