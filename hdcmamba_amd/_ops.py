@@ -45,6 +45,8 @@ _PROTOS = {
                                     c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                     c_int, c_void_p]),
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
+    "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                                     c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
 }
 
 _lib = None
@@ -328,3 +330,44 @@ def chunk_pos_advance(pos_dev, chunk):
     if pos_dev.dtype != torch.int32 or pos_dev.numel() != 1:
         raise RuntimeError("chunk_pos_advance: pos_dev must be a one-element int32 tensor")
     _check("hdcm_chunk_pos_advance", lib().hdcm_chunk_pos_advance(pos_dev.data_ptr(), int(chunk), _stream(pos_dev)))
+
+
+# ----------------------------------------------------------------------------- decode projections
+SKINNY_MAX_ROWS = 16
+SKINNY_MAX_K = 3072
+
+
+def skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether linear(x, weight) at x's shape runs on the skinny decode GEMM: bf16, at most
+    16 rows, K a multiple of 32 up to 3072."""
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and rows <= SKINNY_MAX_ROWS
+            and K % 32 == 0 and K <= SKINNY_MAX_K and weight.shape[-1] == K)
+
+
+def skinny_linear(x, weight, bias=None, residual=None, out=None):
+    """x [..., K] (at most 16 rows) @ weight[N, K]^T (+ bias[N]) (+ residual [..., N]) -> [..., N]
+    on the skinny decode GEMM (bf16, fp32 accumulation).  ``out`` may be ``residual``."""
+    _on_gpu(x, weight)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if out is None:
+        out = torch.empty(*lead, N, device=x.device, dtype=x.dtype)
+    o2 = out.view(-1, N)
+    r2 = residual.reshape(-1, N) if residual is not None else None
+    if bias is not None:
+        bias = _same(bias, x, "bias")
+    ev = timer.begin("skinny_gemm")
+    _check("hdcm_skinny_gemm_fwd", lib().hdcm_skinny_gemm_fwd(
+        x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), bias.data_ptr() if bias is not None else None,
+        r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0, o2.data_ptr(),
+        o2.stride(0), M, N, K, _dtype(x), _stream(x)))
+    timer.end("skinny_gemm", ev)
+    return out

@@ -20,7 +20,8 @@
 //
 // Decode is weight- and state-bandwidth bound (the GEMMs around it read every weight once
 // per step), so these kernels are simple: one workgroup per batch row (norm_conv_step) and
-// one per (head, batch) plus one per batch for the SSM channels (mixer_step).
+// one per (head, batch) plus one per batch for the SSM channels (mixer_step).  Head dims
+// 32, 64, 96 and 128 are built.
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -121,14 +122,21 @@ __global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
 __device__ __forceinline__ float phi_f(float z) { return fexp(fminf(z, 0.f)) + fmaxf(z, 0.f); }
 
 // grid (H + 1, B): x < H is head x's slot step, x == H the SSM channels of batch row b.
-template <typename T>
+// A slot workgroup owns one head's two fp32 states [HD][HD]; thread t holds 4 consecutive
+// columns (float4) of rows t / CG + RGS * k, so every state load of the step is issued
+// before the first use and the row sums of y are finished through LDS.
+template <typename T, int HD>
 __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
-    const T* __restrict__ projs, int64_t prs, int q_col, int dm, int hd, const T* __restrict__ gamma,
+    const T* __restrict__ projs, int64_t prs, int q_col, int dm, const T* __restrict__ gamma,
     float* __restrict__ S_prev, float* __restrict__ S_intra, int c_arg, const int* __restrict__ c_dev, int C,
     const T* __restrict__ gn_w,
     const T* __restrict__ gn_b, float gn_eps, const T* __restrict__ A_log, float* __restrict__ hs,
     int ds, T* __restrict__ out, int64_t ors, int y_col, int g_col) {
-  __shared__ float sq[128], sk[128], sv[128], sy[kThreads];
+  constexpr int CG = HD / 4;              // float4 column groups of a state row
+  constexpr int RGS = kThreads / CG;      // row groups
+  constexpr int RPT = (HD + RGS - 1) / RGS;  // rows per thread
+  __shared__ float sq[HD], sk[HD], sv[HD];
+  __shared__ float sy[RGS][HD + 4];
   __shared__ float red[kWaves * 2];
   const int tid = threadIdx.x, b = blockIdx.y, H = gridDim.x - 1;
   const T* row = projs + (int64_t)b * prs;
@@ -148,12 +156,25 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   }
 
   const int h = blockIdx.x;
+  const int cgi = tid % CG, rg = tid / CG;
+  const bool act = rg < RGS;
+  const int64_t sbase = (((int64_t)b * H + h) * HD) * HD + 4 * cgi;
+  // issue the state loads first
+  float4 sp[RPT], si[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = rg + RGS * k;
+    if (act && i < HD) {
+      sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
+      si[k] = *reinterpret_cast<const float4*>(S_intra + sbase + (int64_t)i * HD);
+    }
+  }
   // chunk offset: from device memory when the step runs inside a captured graph
   const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
   const float g = to_f<T>(gamma[h]);
   const float lg2 = log2f(g);
-  const T* q = row + q_col + h * hd;
-  if (tid < hd) {
+  const T* q = row + q_col + h * HD;
+  if (tid < HD) {
     // phi(q), phi(k) rounded to the activation dtype as in the chunked kernels' operands
     sq[tid] = rnd<T>(phi_f(to_f<T>(q[tid])));
     sk[tid] = rnd<T>(phi_f(to_f<T>(q[dm + tid])));
@@ -161,43 +182,49 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   }
   __syncthreads();
 
-  // thread (rg, j): column j of the state, rows rg, rg + RG, ...
-  const int RG = kThreads / hd;
-  const int rg = tid / hd, j = tid % hd;
-  const bool act = rg < RG;
   const bool first = c == 0, last = c == C - 1;
   const float gc = fexp2((float)c * lg2), gC = fexp2((float)C * lg2);
-  float acc = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (act) {
-    const int64_t base = (((int64_t)b * H + h) * hd) * hd + j;
-    const float vj = sv[j];
-    for (int i = rg; i < hd; i += RG) {
-      const int64_t e = base + (int64_t)i * hd;
-      const float sp = S_prev[e];
-      const float si = (first ? 0.f : g * S_intra[e]) + sk[i] * vj;
-      acc += sq[i] * (si + gc * sp);
+    const float v4[4] = {sv[4 * cgi], sv[4 * cgi + 1], sv[4 * cgi + 2], sv[4 * cgi + 3]};
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      const int i = rg + RGS * k;
+      if (i >= HD) continue;
+      const float ki = sk[i], qi = sq[i];
+      float p[4] = {sp[k].x, sp[k].y, sp[k].z, sp[k].w};
+      float n[4] = {si[k].x, si[k].y, si[k].z, si[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        n[e] = (first ? 0.f : g * n[e]) + ki * v4[e];
+        acc[e] += qi * (n[e] + gc * p[e]);
+      }
+      const int64_t off = sbase + (int64_t)i * HD;
       if (last) {
-        S_prev[e] = gC * sp + si;
-        S_intra[e] = 0.f;
+        *reinterpret_cast<float4*>(S_prev + off) =
+            make_float4(gC * p[0] + n[0], gC * p[1] + n[1], gC * p[2] + n[2], gC * p[3] + n[3]);
+        *reinterpret_cast<float4*>(S_intra + off) = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        S_intra[e] = si;
+        *reinterpret_cast<float4*>(S_intra + off) = make_float4(n[0], n[1], n[2], n[3]);
       }
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sy[rg][4 * cgi + e] = acc[e];
   }
-  sy[tid] = acc;
   __syncthreads();
   float y = 0.f;
-  if (tid < hd) {
-    for (int k = 0; k < RG; ++k) y += sy[k * hd + tid];
+  if (tid < HD) {
+#pragma unroll
+    for (int k = 0; k < RGS; ++k) y += sy[k][tid];
   }
   // GroupNorm over the head's hd values, then the gate
-  float st[2] = {tid < hd ? y : 0.f, tid < hd ? y * y : 0.f};
+  float st[2] = {tid < HD ? y : 0.f, tid < HD ? y * y : 0.f};
   block_sum<2>(st, red);
-  const float mean = st[0] / (float)hd;
-  const float var = fmaxf(st[1] / (float)hd - mean * mean, 0.f);
+  const float mean = st[0] / (float)HD;
+  const float var = fmaxf(st[1] / (float)HD - mean * mean, 0.f);
   const float rinv = rsqrtf(var + gn_eps);
-  if (tid < hd) {
-    const int col = h * hd + tid;
+  if (tid < HD) {
+    const int col = h * HD + tid;
     const float gate = to_f<T>(row[q_col + 3 * dm + col]);
     const float yn = (y - mean) * rinv * to_f<T>(gn_w[col]) + to_f<T>(gn_b[col]);
     orow[g_col + col] = from_f<T>(yn * frcp(1.0f + fexp(-gate)));
@@ -272,25 +299,35 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
   HDCM_CHECK_ARG(y_col >= 0 && g_col >= 0 && out_row_stride >= y_col + ds && out_row_stride >= g_col + dm,
                  HDCM_EINVAL);
   const int64_t hd = dm / H;
-  HDCM_CHECK_ARG(hd <= 128 && H < 65535 && B <= 65535 && proj_row_stride < ((int64_t)1 << 31),
+  HDCM_CHECK_ARG((hd == 32 || hd == 64 || hd == 96 || hd == 128) && H < 65535 && B <= 65535 &&
+                     proj_row_stride < ((int64_t)1 << 31),
                  HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(C < ((int64_t)1 << 24), HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(hdcm_aligned16(S_prev) && hdcm_aligned16(S_intra), HDCM_EALIGN);
   if (B == 0) return HDCM_OK;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(H + 1), (unsigned)B);
-  if (dtype == HDCM_F32)
-    hipLaunchKernelGGL((mixer_step_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs,
-                       proj_row_stride, (int)q_col, (int)dm, (int)hd, (const float*)gamma, S_prev, S_intra,
-                       (int)pos, (const int*)pos_dev, (int)C, (const float*)gn_w, (const float*)gn_b, gn_eps,
-                       (const float*)A_log, h, (int)ds, (float*)out, out_row_stride, (int)y_col,
-                       (int)g_col);
-  else
-    hipLaunchKernelGGL((mixer_step_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs,
-                       proj_row_stride, (int)q_col, (int)dm, (int)hd, (const bf16_t*)gamma, S_prev,
-                       S_intra, (int)pos, (const int*)pos_dev, (int)C, (const bf16_t*)gn_w, (const bf16_t*)gn_b, gn_eps,
-                       (const bf16_t*)A_log, h, (int)ds, (bf16_t*)out, out_row_stride, (int)y_col,
-                       (int)g_col);
-  return hdcm_launch_status();
+#define HDCM_MIX_CASE(TT, HDV)                                                                              \
+  if (hd == HDV) {                                                                                           \
+    hipLaunchKernelGGL((mixer_step_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)projs,          \
+                       proj_row_stride, (int)q_col, (int)dm, (const TT*)gamma, S_prev, S_intra, (int)pos,    \
+                       (const int*)pos_dev, (int)C, (const TT*)gn_w, (const TT*)gn_b, gn_eps,               \
+                       (const TT*)A_log, h, (int)ds, (TT*)out, out_row_stride, (int)y_col, (int)g_col);      \
+    return hdcm_launch_status();                                                                             \
+  }
+  if (dtype == HDCM_F32) {
+    HDCM_MIX_CASE(float, 32)
+    HDCM_MIX_CASE(float, 64)
+    HDCM_MIX_CASE(float, 96)
+    HDCM_MIX_CASE(float, 128)
+  } else {
+    HDCM_MIX_CASE(bf16_t, 32)
+    HDCM_MIX_CASE(bf16_t, 64)
+    HDCM_MIX_CASE(bf16_t, 96)
+    HDCM_MIX_CASE(bf16_t, 128)
+  }
+#undef HDCM_MIX_CASE
+  return HDCM_EUNSUPPORTED;
 }
 
 extern "C" int hdcm_chunk_pos_advance(int32_t* pos_dev, int64_t C, void* stream) {

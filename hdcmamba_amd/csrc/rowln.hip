@@ -16,8 +16,11 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kRows = 4;
+// Below this many rows (decode steps: one row per sequence) every row gets its own
+// single-wave workgroup, so the rows spread over CUs instead of queueing in one wave.
+constexpr int64_t kFewRows = 4096;
 
-template <typename T, int NG, bool AFFINE>
+template <typename T, int NG, bool AFFINE, int kRows, int kWavesPerBlock>
 __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
     const T* in, int64_t in_rs, T* out, int64_t out_rs, const T* __restrict__ w,
     const T* __restrict__ b, int64_t rows, int W, float eps) {
@@ -85,19 +88,28 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
   }
 }
 
-template <typename T, int NG>
-int launch_ng(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
-              const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
-  const int64_t per_block = (int64_t)kWavesPerBlock * kRows;
+template <typename T, int NG, int R, int WPB>
+void launch_shape(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
+                  const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
+  const int64_t per_block = (int64_t)WPB * R;
   dim3 grid((unsigned)((rows + per_block - 1) / per_block));
   if (w)
-    hipLaunchKernelGGL((rowln_kernel<T, NG, true>), grid, dim3(kWavesPerBlock * kWave), 0, s,
+    hipLaunchKernelGGL((rowln_kernel<T, NG, true, R, WPB>), grid, dim3(WPB * kWave), 0, s,
                        (const T*)in, in_rs, (T*)out, out_rs, (const T*)w, (const T*)b, rows, (int)W,
                        eps);
   else
-    hipLaunchKernelGGL((rowln_kernel<T, NG, false>), grid, dim3(kWavesPerBlock * kWave), 0, s,
+    hipLaunchKernelGGL((rowln_kernel<T, NG, false, R, WPB>), grid, dim3(WPB * kWave), 0, s,
                        (const T*)in, in_rs, (T*)out, out_rs, (const T*)nullptr,
                        (const T*)nullptr, rows, (int)W, eps);
+}
+
+template <typename T, int NG>
+int launch_ng(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
+              const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
+  if (rows < kFewRows)
+    launch_shape<T, NG, 1, 1>(in, in_rs, out, out_rs, w, b, rows, W, eps, s);
+  else
+    launch_shape<T, NG, kRows, kWavesPerBlock>(in, in_rs, out, out_rs, w, b, rows, W, eps, s);
   return hdcm_launch_status();
 }
 

@@ -1,0 +1,128 @@
+// Skinny bf16 GEMM for the single-token decode step on gfx950:
+//   out[m, n] = sum_k A[m, k] W[n, k]  (+ bias[n])  (+ res[m, n]),   m < M <= 16
+// with W an nn.Linear weight [N, K] (K contiguous).  It replaces the decode step's
+// projections (in_proj with its bias, out_proj with the residual add, the tied LM head;
+// hdcmamba/model.py:313,325,340,383 and train_fineweb.py:55,94 run them as nn.Linear).
+//
+// At M = 16 every weight is read once per step and used for 16 rows only, so the GEMM is
+// bound by streaming W from HBM.  A workgroup of four waves owns one 16-column tile of
+// the output; its waves split K four ways and each issues all of its W loads (one 16-byte
+// fragment per lane per K=32 step, 16 rows x 64 contiguous bytes per instruction) before
+// the first v_mfma_f32_16x16x32_bf16, so a wave keeps its whole share of W in flight.  A
+// (the 16 activation rows, a few tens of KB) is read from L2 the same way.  The four partial
+// 16x16 tiles are summed through LDS and the epilogue adds bias and residual in fp32 and
+// rounds once to bf16.
+#include "hdcm_common.h"
+
+using namespace hdcm;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxSteps = 24;  // K=32 steps per wave: K <= 4 * 24 * 32 = 3072
+
+template <int STEPS, bool BIAS, bool RES>
+__global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
+    const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
+    const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
+    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K) {
+  __shared__ float part[kWaves][16][17];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nsteps = K / 32;
+  // contiguous K ranges per wave: the first (nsteps % 4) waves take one step more
+  const int base = nsteps / kWaves, extra = nsteps % kWaves;
+  const int my = base + (w < extra ? 1 : 0);
+  const int s0 = w * base + (w < extra ? w : extra);
+
+  // A fragments: lane (m = l16, g) holds A[m][32 s + 8 g .. +8]; rows past M read row 0.
+  // B fragments: lane (n = l16, g) holds W[n0 + n][32 s + 8 g .. +8]; rows past N read row
+  // N-1 (their outputs are not stored).  Every load of the wave is issued before the first
+  // MFMA (A first: it is L2-resident and returns ahead of W), so the wave waits for one
+  // memory round trip instead of one per K step.
+  const int am = l16 < M ? l16 : 0;
+  const bf16_t* ap = A + (int64_t)am * a_rs + 8 * g;
+  const int wn = min(n0 + l16, N - 1);
+  const bf16_t* wp = W + (int64_t)wn * w_rs + 8 * g;
+  Frag<bf16_t> fa[STEPS], bw[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+    if (s < my) fa[s].v = *reinterpret_cast<const bf16x8_t*>(ap + 32 * (s0 + s));
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+    if (s < my) bw[s].v = *reinterpret_cast<const bf16x8_t*>(wp + 32 * (s0 + s));
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+    if (s < my) acc = mma(fa[s], bw[s], acc);
+  // D layout: lane holds D[4 g + r][l16]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
+  __syncthreads();
+  if (w == 0) {
+    const int n = n0 + l16;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * g + r;
+      float v = part[0][m][l16] + part[1][m][l16] + part[2][m][l16] + part[3][m][l16];
+      if (m < M && n < N) {
+        if (BIAS) v += bf2f(bias[n]);
+        if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
+        out[(int64_t)m * o_rs + n] = f2bf(v);
+      }
+    }
+  }
+}
+
+template <int STEPS>
+void launch_steps(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
+                  int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
+  bf16_t* o = (bf16_t*)out;
+  if (bias && res)
+    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, true, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs, bs,
+                       rs, r_rs, o, o_rs, M, N, K);
+  else if (bias)
+    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, true, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K);
+  else if (res)
+    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt,
+                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K);
+}
+
+}  // namespace
+
+extern "C" int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const void* W, int64_t w_row_stride,
+                                    const void* bias, const void* res, int64_t res_row_stride, void* out,
+                                    int64_t out_row_stride, int64_t M, int64_t N, int64_t K, int dtype,
+                                    void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(A && W && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(M >= 0 && N >= 0 && K > 0, HDCM_EINVAL);
+  HDCM_CHECK_ARG(a_row_stride >= K && w_row_stride >= K && out_row_stride >= N, HDCM_EINVAL);
+  HDCM_CHECK_ARG(!res || res_row_stride >= N, HDCM_EINVAL);
+  HDCM_CHECK_ARG(M <= 16 && K % 32 == 0 && K <= (int64_t)kWaves * kMaxSteps * 32, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(N < ((int64_t)1 << 30), HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(hdcm_aligned16(A) && hdcm_aligned16(W) && a_row_stride % 8 == 0 && w_row_stride % 8 == 0,
+                 HDCM_EALIGN);
+  if (M == 0 || N == 0) return HDCM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int steps = (int)((K / 32 + kWaves - 1) / kWaves);
+  const int m = (int)M, n = (int)N, k = (int)K;
+  if (steps <= 8)
+    launch_steps<8>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+  else if (steps <= 12)
+    launch_steps<12>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+  else if (steps <= 18)
+    launch_steps<18>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+  else
+    launch_steps<kMaxSteps>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m,
+                            n, k, s);
+  return hdcm_launch_status();
+}

@@ -190,13 +190,19 @@ class HdcMamba9v3Block(nn.Module):
         dtype = x.dtype
         xc = _ops.norm_conv_step(x, self.norm.weight, self.norm.bias, self.conv1d.weight.squeeze(1),
                                  self.conv1d.bias, self.norm.eps, state.conv)
-        projs = F.linear(xc, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
+        w_in, b_in = self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype)
+        # few rows: the weight-streaming skinny GEMM; otherwise the library GEMM
+        projs = _ops.skinny_linear(xc, w_in, b_in) if _ops.skinny_ok(xc, w_in) else F.linear(xc, w_in, b_in)
         combined = torch.empty(B, ds + dm, device=x.device, dtype=dtype)
         _ops.mixer_step(projs, self.A_log, ds, 3 * ds, self.gamma_buf.to(dtype), self.group_norm.weight,
                         self.group_norm.bias, 1e-5, state.h, state.S_prev, state.S_intra, state.pos, C,
                         combined, dm, H, pos_dev=pos_dev)
         _ops.layer_norm(combined, eps=1e-5, out=combined)
-        y = torch.addmm(x, combined, self.out_proj.weight.to(dtype).t())
+        w_out = self.out_proj.weight.to(dtype)
+        if _ops.skinny_ok(combined, w_out):
+            y = _ops.skinny_linear(combined, w_out, residual=x)
+        else:
+            y = torch.addmm(x, combined, w_out.t())
         if pos_dev is None:
             state.pos = (state.pos + 1) % C
         return y

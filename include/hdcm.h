@@ -126,7 +126,8 @@ int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col
  * S_intra [B,H,hd,hd] (this chunk's tokens so far; zero at a chunk start), both fp32 and
  * updated; pos = t mod C is the token's offset in its chunk (0 right after a prefill,
  * whose padded length is a multiple of C).  Writes y_ssm to columns [y_col, y_col+ds) and
- * the gated slot output to [g_col, g_col+dm) of out.  Needs hd <= 128.  With pos_dev
+ * the gated slot output to [g_col, g_col+dm) of out.  Needs hd in {32,64,96,128} and
+ * 16-byte aligned S_prev / S_intra.  With pos_dev
  * non-NULL the offset is read from that device int32 instead of pos, so one captured
  * graph of a decode step serves every position; hdcm_chunk_pos_advance then moves it to
  * (pos + 1) mod C on the stream (no counterpart in the reference: graph replay support).
@@ -142,6 +143,21 @@ int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, int64_t q_co
                         int64_t out_row_stride, int64_t y_col, int64_t g_col, int64_t B,
                         int64_t dm, int64_t ds, int64_t H, int dtype, void* stream);
 int hdcm_chunk_pos_advance(int32_t* pos_dev, int64_t C, void* stream);
+
+/*
+ * Skinny bf16 GEMM of the decode step: out[m,n] = sum_k A[m,k] W[n,k] (+ bias[n])
+ * (+ res[m,n]) for m < M <= 16, fp32 accumulation, one rounding to bf16.  W is an
+ * nn.Linear weight [N,K] (row stride w_row_stride); bias [N] and res (row stride
+ * res_row_stride) may be NULL; res may alias out.  Needs K % 32 == 0, K <= 3072 and
+ * 16-byte aligned rows of A and W.
+ * Replaces, in the decode step only, the nn.Linear projections in_proj and out_proj
+ * (hdcmamba/model.py:313,325,340,383; the residual add of model.py:394) and the tied LM
+ * head (train_fineweb.py:55,94).
+ */
+int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const void* W, int64_t w_row_stride,
+                         const void* bias, const void* res, int64_t res_row_stride, void* out,
+                         int64_t out_row_stride, int64_t M, int64_t N, int64_t K, int dtype,
+                         void* stream);
 
 /*
  * Row LayerNorm over `width` columns, fp32 statistics, optional affine

@@ -134,6 +134,28 @@ def test_decode_step_validation():
     assert lib.hdcm_chunk_pos_advance(None, 64, None) == EINVAL
 
 
+def test_skinny_gemm_validation():
+    # hdcm_skinny_gemm_fwd(A, a_rs, W, w_rs, bias, res, res_rs, out, o_rs, M, N, K, dtype, stream)
+    f = _ops.lib().hdcm_skinny_gemm_fwd
+    base = [P16, 2048, P16, 2048, None, None, 0, P16, 8576, 16, 8576, 2048, 1, None]
+    a = list(base); a[12] = 0  # fp32 is not built (decode in fp32 stays on the library GEMM)
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[9] = 17  # more than 16 rows
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[11] = 2040; a[1] = a[3] = 2040  # K not a multiple of 32
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[11] = 4096; a[1] = a[3] = 4096  # K beyond the per-wave register share
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[2] = None
+    assert f(*a) == EINVAL
+    a = list(base); a[8] = 100  # output row shorter than N
+    assert f(*a) == EINVAL
+    a = list(base); a[1] = 2052; a[3] = 2052  # rows not 16-byte aligned
+    assert f(*a) == EALIGN
+    a = list(base); a[9] = 0
+    assert f(*a) == OK
+
+
 def test_rowln_validation():
     f = _ops.lib().hdcm_rowln_fwd
     base = [P16, 1152, P16, 1152, None, None, 10, 1152, 1e-5, 1, None]

@@ -155,3 +155,48 @@ def test_slot_unsupported_head_dim(dev):
     projs, gamma, gn_w, gn_b = slot_inputs(1, 64, 240, 64, 5, torch.bfloat16)  # hd 48
     with pytest.raises(_ops.HdcmError):
         _run_slot(dev, projs, gamma, gn_w, gn_b, 240, 64, 5, 64)
+
+
+# ----------------------------------------------------------------------------- skinny decode GEMM
+@pytest.mark.parametrize("M,N,K,bias,res", [
+    (16, 8576, 2048, True, False),    # d_model 2048 in_proj of a B=16 decode step
+    (16, 2048, 2176, False, True),    # its out_proj with the residual add
+    (16, 50304, 2048, False, False),  # the tied LM head
+    (7, 3264, 768, True, False),
+    (16, 768, 832, False, True),
+    (1, 100, 64, True, True),
+    (5, 33, 3072, False, False),
+])
+def test_skinny_gemm(dev, M, N, K, bias, res):
+    """bf16 operands, fp32 accumulation, one rounding: against torch fp32 on the same
+    bf16 operands (max error a bf16 rounding of the result plus fp32 summation order)."""
+    _say("skinny", M, N, K, bias, res)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16) if bias else None
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16) if res else None
+    ref = A.float() @ W.float().t()
+    if bias:
+        ref = ref + b.float()
+    if res:
+        ref = ref + r.float()
+    out = _ops.skinny_linear(A.to(dev), W.to(dev), None if b is None else b.to(dev),
+                             None if r is None else r.to(dev))
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 1e-3).all(), f"max err {err.max().item()}"
+
+
+def test_skinny_gemm_in_place_residual(dev):
+    """out may be the residual buffer itself."""
+    g = torch.Generator().manual_seed(3)
+    A = torch.randn(16, 512, generator=g).to(torch.bfloat16).to(dev)
+    W = (torch.randn(256, 512, generator=g) / 512 ** 0.5).to(torch.bfloat16).to(dev)
+    r = torch.randn(16, 256, generator=g).to(torch.bfloat16).to(dev)
+    ref = (A.float() @ W.float().t() + r.float()).cpu()
+    out = _ops.skinny_linear(A, W, residual=r, out=r)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == r.data_ptr()
+    err = (r.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 1e-3).all()
