@@ -4,11 +4,13 @@
 Default workload: the 24-layer d_model=1024 (d_state 128, 16 heads, chunk 64, vocab 50304,
 tied head) language model forward at B=1, L=32768 in bf16, uniform random token ids and
 random-init weights.  One step = one full forward (embedding, 24 blocks, final norms,
-logits).  Prints ONE JSON line with tokens/s, the roofline of the dominant custom kernel
-(measured with HIP events on the launch stream during the timed steps), per-kernel
+logits), timed as replays of the forward recorded as a HIP graph.  Prints ONE JSON line
+with tokens/s, the roofline of the dominant custom kernel (HIP events on the launch stream
+around each custom kernel, over a second timed region of eager forwards), per-kernel
 figures, and the CPU oracle's throughput on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2]
+    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2|lm_c5_decode]
+                    [--graph on|off] [--tuned-gemms on|off] [--cpu-baseline on|off]
 """
 from __future__ import annotations
 

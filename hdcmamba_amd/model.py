@@ -116,9 +116,11 @@ class HdcMamba9v3Block(nn.Module):
         projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
         combined = torch.empty(B, L, ds + dm, device=x.device, dtype=dtype)
         # The SSM (latency-bound: three short launches) and the slot kernels read projs
-        # and write disjoint columns of `combined`, so the SSM runs on a side stream and
-        # overlaps the slot passes.  The join below orders every later use (and the
-        # allocator's reuse) of projs and combined after it.
+        # and write disjoint columns of `combined`, so the SSM runs on a side stream next
+        # to the slot state pre-pass and scan.  It joins before slot_gate, which then has
+        # the GPU to itself (overlapping the gate as well measured the same forward time
+        # within noise).  The join orders every later use (and the allocator's reuse) of
+        # projs and combined after the SSM.
         main = torch.cuda.current_stream(x.device)
         side = _ops.side_stream(x.device)
         side.wait_stream(main)
@@ -128,9 +130,9 @@ class HdcMamba9v3Block(nn.Module):
         q_col = 3 * ds
         ws = _ops.slot_workspace(projs, dm, H, C)
         _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
+        main.wait_stream(side)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
                        combined, ds, dm, H, C, S_final=None if state is None else state.S_prev)
-        main.wait_stream(side)
         _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
 
