@@ -63,11 +63,10 @@ class HdcMambaLM(nn.Module):
         return self.lm_head(x)
 
     def _logits(self, x):
-        """norm_f then the tied head; a few rows (decode steps, the last prefill position)
-        run on the skinny GEMM."""
+        """norm_f then the tied head.  The head stays on the library GEMM even for the few
+        rows of a decode step: at V=50304 it streams 206 MB and hipBLASLt's skinny solution
+        runs it in about 48 us against 55 us on the skinny decode kernel."""
         x = _ops.layer_norm(x.contiguous(), self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
-        if _ops.skinny_ok(x, self.lm_head.weight):
-            return _ops.skinny_linear(x, self.lm_head.weight)
         return self.lm_head(x)
 
     def prefill(self, input_ids, last=1):
