@@ -47,6 +47,10 @@ _PROTOS = {
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
     "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                      c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_norm_conv_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
+    "hdcm_norm_conv_bwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_size_t, c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
 }
 
 _lib = None
@@ -187,6 +191,31 @@ def norm_conv(x, ln_w, ln_b, conv_w, conv_b, eps, out=None):
         _dtype(x), _stream(x)))
     timer.end("norm_conv", ev)
     return out
+
+
+def norm_conv_bwd(grad_out, x, ln_w, ln_b, conv_w, eps):
+    """Gradients of norm_conv: returns dx (x.dtype, [B,L,D]) and fp32 d_ln_w [D],
+    d_ln_b [D], d_conv_w [D,4], d_conv_b [D]."""
+    _on_gpu(grad_out, x)
+    B, L, D = x.shape
+    ln_w = _same(ln_w, x, "ln_w")
+    ln_b = _same(ln_b, x, "ln_b")
+    conv_w = _same(conv_w.reshape(D, 4), x, "conv_w")
+    grad_out = _same(grad_out, x, "grad_out")
+    if x.stride(2) != 1:
+        x = x.contiguous()
+    dx = torch.empty(B, L, D, device=x.device, dtype=x.dtype)
+    f32 = dict(device=x.device, dtype=torch.float32)
+    d_ln_w, d_ln_b, d_conv_b = torch.empty(D, **f32), torch.empty(D, **f32), torch.empty(D, **f32)
+    d_conv_w = torch.empty(D, 4, **f32)
+    nbytes = lib().hdcm_norm_conv_bwd_workspace_bytes(B, L, D)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+    _check("hdcm_norm_conv_bwd", lib().hdcm_norm_conv_bwd(
+        grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), x.data_ptr(), x.stride(0), x.stride(1),
+        ln_w.data_ptr(), ln_b.data_ptr(), conv_w.data_ptr(), dx.data_ptr(), dx.stride(0), dx.stride(1),
+        d_ln_w.data_ptr(), d_ln_b.data_ptr(), d_conv_w.data_ptr(), d_conv_b.data_ptr(), ws.data_ptr(), nbytes,
+        B, L, D, float(eps), _dtype(x), _stream(x)))
+    return dx, d_ln_w, d_ln_b, d_conv_w, d_conv_b
 
 
 def ssm(projs, A_log, d_state, y, h0=None, h_final=None):

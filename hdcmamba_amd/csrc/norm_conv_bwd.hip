@@ -1,0 +1,355 @@
+// Backward of the fused LayerNorm + causal depthwise conv (width 4) for gfx950.
+//
+// Forward (norm_conv.hip; hdcmamba/model.py:22-72): xh[t] = (x[t] - mu_t) * r_t,
+// u[t] = xh[t] * g + b for t >= 0 and u[t] = b for t < 0 (the LayerNorm of a zero row),
+// out[t] = sum_k w_k u[t-3+k] + cb.  With go = dL/dout this computes the exact gradients
+// of that forward (hdcmamba/model.py:74-166 is the reference's backward, which drops the
+// b terms of dw and db and works from bf16-rounded statistics; see the oracle):
+//   gu[t]  = sum_k w_k go[t+3-k]                     (t >= 0; go past L is 0)
+//   dx[t]  = r_t (gh - mean(gh) - xh[t] mean(gh xh[t])),  gh = gu[t] g
+//   dg     = sum_{t>=0} gu[t] xh[t]
+//   db     = sum_{t>=0} gu[t] + sum_{t, k: t-3+k<0} w_k go[t]
+//   dcb    = sum_t go[t]
+//   dw_k   = sum_t go[t] u[t-3+k]
+//
+// norm_conv_bwd_rows_kernel: one wave per 16-row run, lanes own 16-byte column groups (as
+// the forward); a ring holds go[t..t+3]; writes dx and the row statistics (mu_t, r_t).
+// norm_conv_bwd_cols_kernel: thread = one 16-byte column group x one chunk of rows; walks
+// the chunk keeping go[t..t+3] and u[t-3..t] in registers and writes the seven column sums
+// of its chunk.  norm_conv_bwd_reduce_kernel sums the chunks in a fixed order (the result
+// does not depend on scheduling).
+#include "hdcm_common.h"
+
+using namespace hdcm;
+
+namespace {
+
+constexpr int kRowsWPB = 4;   // waves per workgroup, rows kernel
+constexpr int kRunRows = 16;  // rows per wave, rows kernel
+constexpr int kChunk = 256;   // rows per chunk, column kernel
+constexpr int kColThreads = 64;
+
+template <typename T, int NG>
+__device__ __forceinline__ void ld_row(float (&v)[NG][Vec<T>::N], const T* row, int lane, int G, bool valid) {
+  constexpr int E = Vec<T>::N;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = lane + kWave * i;
+    if (valid && g < G) {
+      load16<T>(row + (int64_t)g * E, v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] = 0.f;
+    }
+  }
+}
+
+template <typename T, int NG>
+__global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
+    const T* __restrict__ go, int64_t g_bs, int64_t g_rs, const T* __restrict__ x, int64_t x_bs, int64_t x_rs,
+    const T* __restrict__ ln_w, const T* __restrict__ conv_w, T* __restrict__ dx, int64_t d_bs, int64_t d_rs,
+    float2* __restrict__ stats, int L, int D, float eps) {
+  constexpr int E = Vec<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t t0 = ((int64_t)blockIdx.x * kRowsWPB + wave) * kRunRows;
+  if (t0 >= L) return;
+  const int b = blockIdx.y;
+  const int G = D / E;
+  const float invD = 1.0f / (float)D;
+  const T* gb = go + (int64_t)b * g_bs;
+  const T* xb = x + (int64_t)b * x_bs;
+  T* db = dx + (int64_t)b * d_bs;
+
+  float gw[NG][E], cw[4][NG][E];
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = lane + kWave * i;
+    float c4[4 * E];
+    if (g < G) {
+      load16<T>(ln_w + g * E, gw[i]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)g * E * 4 + k * E, c4 + k * E);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) gw[i][e] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4 * E; ++e) c4[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cw[k][i][e] = c4[4 * e + k];
+  }
+
+  // go ring: r0 = go[t], r1 = go[t+1], r2 = go[t+2]; go[t+3] is loaded each row
+  float r0[NG][E], r1[NG][E], r2[NG][E];
+  ld_row<T, NG>(r0, gb + t0 * g_rs, lane, G, true);
+  ld_row<T, NG>(r1, gb + (t0 + 1) * g_rs, lane, G, t0 + 1 < L);
+  ld_row<T, NG>(r2, gb + (t0 + 2) * g_rs, lane, G, t0 + 2 < L);
+
+#pragma unroll 1
+  for (int r = 0; r < kRunRows; ++r) {
+    const int64_t t = t0 + r;
+    if (t >= L) break;
+    float r3[NG][E], xv[NG][E];
+    ld_row<T, NG>(r3, gb + (t + 3) * g_rs, lane, G, t + 3 < L);
+    ld_row<T, NG>(xv, xb + t * x_rs, lane, G, true);
+    // row statistics of x[t]
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) s += xv[i][e];
+    const float mean = wave_total(s) * invD;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const bool ok = (lane + kWave * i) < G;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float c = ok ? xv[i][e] - mean : 0.f;
+        xv[i][e] = c;
+        q += c * c;
+      }
+    }
+    const float rstd = rsqrtf(wave_total(q) * invD + eps);
+    // gh = (sum_k w_k go[t+3-k]) * g, and the two row sums of the LayerNorm backward
+    float gh[NG][E];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float gu = cw[3][i][e] * r0[i][e] + cw[2][i][e] * r1[i][e] + cw[1][i][e] * r2[i][e] +
+                         cw[0][i][e] * r3[i][e];
+        gh[i][e] = gu * gw[i][e];
+        xv[i][e] *= rstd;  // xh
+        s1 += gh[i][e];
+        s2 += gh[i][e] * xv[i][e];
+      }
+    const float m1 = wave_total(s1) * invD, m2 = wave_total(s2) * invD;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int g = lane + kWave * i;
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = rstd * (gh[i][e] - m1 - xv[i][e] * m2);
+      if (g < G) store16<T>(db + t * d_rs + (int64_t)g * E, o);
+    }
+    if (lane == 0) stats[(int64_t)b * L + t] = make_float2(mean, rstd);
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        r0[i][e] = r1[i][e];
+        r1[i][e] = r2[i][e];
+        r2[i][e] = r3[i][e];
+      }
+  }
+}
+
+// part layout per chunk: [7][D] = dg, db, dcb, dw0, dw1, dw2, dw3
+template <typename T>
+__global__ __launch_bounds__(kColThreads) void norm_conv_bwd_cols_kernel(
+    const T* __restrict__ go, int64_t g_bs, int64_t g_rs, const T* __restrict__ x, int64_t x_bs, int64_t x_rs,
+    const T* __restrict__ ln_w, const T* __restrict__ ln_b, const T* __restrict__ conv_w,
+    const float2* __restrict__ stats, float* __restrict__ part, int L, int D, int nchunk) {
+  constexpr int E = Vec<T>::N;
+  const int G = D / E;
+  const int gi = blockIdx.x * kColThreads + threadIdx.x;
+  const int chunk = blockIdx.y, b = blockIdx.z;
+  if (gi >= G) return;
+  const int c0 = gi * E;
+  const int t0 = chunk * kChunk;
+  const int t1 = min(L, t0 + kChunk);
+  const T* gb = go + (int64_t)b * g_bs + c0;
+  const T* xb = x + (int64_t)b * x_bs + c0;
+  const float2* st = stats + (int64_t)b * L;
+
+  float gw[E], gbias[E], cw[4][E];
+  {
+    float c4[4 * E];
+    load16<T>(ln_w + c0, gw);
+    load16<T>(ln_b + c0, gbias);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)c0 * 4 + k * E, c4 + k * E);
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cw[k][e] = c4[4 * e + k];
+  }
+  auto xh_of = [&](int t, float (&xh)[E]) {  // (x[t] - mu_t) r_t
+    float xv[E];
+    load16<T>(xb + (int64_t)t * x_rs, xv);
+    const float2 s = st[t];
+#pragma unroll
+    for (int e = 0; e < E; ++e) xh[e] = (xv[e] - s.x) * s.y;
+  };
+  auto u_of = [&](int t, float (&u)[E]) {  // u[t] = xh[t] g + b, or b before the sequence start
+    if (t < 0) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) u[e] = gbias[e];
+      return;
+    }
+    float xh[E];
+    xh_of(t, xh);
+#pragma unroll
+    for (int e = 0; e < E; ++e) u[e] = xh[e] * gw[e] + gbias[e];
+  };
+  auto go_of = [&](int t, float (&g)[E]) {
+    if (t < L) {
+      load16<T>(gb + (int64_t)t * g_rs, g);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) g[e] = 0.f;
+    }
+  };
+
+  float acc[7][E];
+#pragma unroll
+  for (int j = 0; j < 7; ++j)
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[j][e] = 0.f;
+  float u3[E], u2[E], u1[E];  // u[t-3], u[t-2], u[t-1]
+  u_of(t0 - 3, u3);
+  u_of(t0 - 2, u2);
+  u_of(t0 - 1, u1);
+  float g0[E], g1[E], g2[E];  // go[t], go[t+1], go[t+2]
+  go_of(t0, g0);
+  go_of(t0 + 1, g1);
+  go_of(t0 + 2, g2);
+#pragma unroll 1
+  for (int t = t0; t < t1; ++t) {
+    float g3[E], xh[E];
+    go_of(t + 3, g3);
+    xh_of(t, xh);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float u0 = xh[e] * gw[e] + gbias[e];
+      const float gu = cw[3][e] * g0[e] + cw[2][e] * g1[e] + cw[1][e] * g2[e] + cw[0][e] * g3[e];
+      acc[0][e] += gu * xh[e];      // dg
+      acc[1][e] += gu;              // db (rows t >= 0)
+      acc[2][e] += g0[e];           // dcb
+      acc[3][e] += g0[e] * u3[e];   // dw0
+      acc[4][e] += g0[e] * u2[e];   // dw1
+      acc[5][e] += g0[e] * u1[e];   // dw2
+      acc[6][e] += g0[e] * u0;      // dw3
+      u3[e] = u2[e];
+      u2[e] = u1[e];
+      u1[e] = u0;
+    }
+    // the b of the rows before the sequence start feeds out[t] for t < 3
+    if (t < 3) {
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          if (t - 3 + k < 0) acc[1][e] += cw[k][e] * g0[e];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      g0[e] = g1[e];
+      g1[e] = g2[e];
+      g2[e] = g3[e];
+    }
+  }
+  float* pp = part + ((int64_t)b * nchunk + chunk) * 7 * D + c0;
+#pragma unroll
+  for (int j = 0; j < 7; ++j)
+#pragma unroll
+    for (int e = 0; e < E; ++e) pp[(int64_t)j * D + e] = acc[j][e];
+}
+
+// out[j][c] = sum over (batch, chunk) of part[..][j][c]; j: dg, db, dcb, dw0..dw3.
+__global__ __launch_bounds__(256) void norm_conv_bwd_reduce_kernel(const float* __restrict__ part, int nparts,
+                                                                   int D, float* __restrict__ d_ln_w,
+                                                                   float* __restrict__ d_ln_b,
+                                                                   float* __restrict__ d_conv_w,
+                                                                   float* __restrict__ d_conv_b) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= 7 * D) return;
+  const int j = idx / D, c = idx % D;
+  float s = 0.f;
+  for (int p = 0; p < nparts; ++p) s += part[(int64_t)p * 7 * D + idx];
+  if (j == 0) d_ln_w[c] = s;
+  else if (j == 1) d_ln_b[c] = s;
+  else if (j == 2) d_conv_b[c] = s;
+  else d_conv_w[(int64_t)c * 4 + (j - 3)] = s;
+}
+
+int64_t chunks_of(int64_t L) { return (L + kChunk - 1) / kChunk; }
+
+template <typename T>
+int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_t x_bs, int64_t x_rs,
+               const void* ln_w, const void* ln_b, const void* conv_w, void* dx, int64_t d_bs, int64_t d_rs,
+               float* d_ln_w, float* d_ln_b, float* d_conv_w, float* d_conv_b, void* ws, int64_t B, int64_t L,
+               int64_t D, float eps, hipStream_t s) {
+  constexpr int E = Vec<T>::N;
+  const int G = (int)(D / E);
+  const int ng = (G + kWave - 1) / kWave;
+  float2* stats = (float2*)ws;
+  float* part = (float*)((char*)ws + ((B * L * sizeof(float2) + 255) / 256) * 256);
+  const int64_t nchunk = chunks_of(L);
+  const dim3 rgrid((unsigned)((L + kRowsWPB * kRunRows - 1) / (kRowsWPB * kRunRows)), (unsigned)B);
+#define HDCM_BWD_ROWS(N)                                                                                         \
+  if (ng == N)                                                                                                   \
+    hipLaunchKernelGGL((norm_conv_bwd_rows_kernel<T, N>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
+                       g_bs, g_rs, (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)conv_w, (T*)dx, d_bs, d_rs, \
+                       stats, (int)L, (int)D, eps);
+  HDCM_BWD_ROWS(1)
+  else HDCM_BWD_ROWS(2) else HDCM_BWD_ROWS(3) else HDCM_BWD_ROWS(4) else return HDCM_EUNSUPPORTED;
+#undef HDCM_BWD_ROWS
+  int st = hdcm_launch_status();
+  if (st) return st;
+  const dim3 cgrid((unsigned)((G + kColThreads - 1) / kColThreads), (unsigned)nchunk, (unsigned)B);
+  hipLaunchKernelGGL((norm_conv_bwd_cols_kernel<T>), cgrid, dim3(kColThreads), 0, s, (const T*)go, g_bs, g_rs,
+                     (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,
+                     (const float2*)stats, part, (int)L, (int)D, (int)nchunk);
+  st = hdcm_launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(norm_conv_bwd_reduce_kernel, dim3((unsigned)((7 * D + 255) / 256)), dim3(256), 0, s,
+                     (const float*)part, (int)(B * nchunk), (int)D, d_ln_w, d_ln_b, d_conv_w, d_conv_b);
+  return hdcm_launch_status();
+}
+
+}  // namespace
+
+extern "C" size_t hdcm_norm_conv_bwd_workspace_bytes(int64_t B, int64_t L, int64_t D) {
+  if (B <= 0 || L <= 0 || D <= 0) return 0;
+  return (size_t)((B * L * sizeof(float2) + 255) / 256) * 256 + (size_t)B * chunks_of(L) * 7 * D * sizeof(float);
+}
+
+extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_row_stride,
+                                  const void* x, int64_t x_batch_stride, int64_t x_row_stride, const void* ln_w,
+                                  const void* ln_b, const void* conv_w, void* dx, int64_t dx_batch_stride,
+                                  int64_t dx_row_stride, float* d_ln_w, float* d_ln_b, float* d_conv_w,
+                                  float* d_conv_b, void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t D,
+                                  float eps, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(grad_out && x && ln_w && ln_b && conv_w && dx && d_ln_w && d_ln_b && d_conv_w && d_conv_b,
+                 HDCM_EINVAL);
+  HDCM_CHECK_ARG(B >= 0 && L >= 0 && D > 0, HDCM_EINVAL);
+  const int E = 16 / hdcm_elt_size(dtype);
+  HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(D / E <= 4 * kWave, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30 && (L + kChunk - 1) / kChunk <= 65535, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(g_row_stride >= D && x_row_stride >= D && dx_row_stride >= D, HDCM_EINVAL);
+  HDCM_CHECK_ARG(g_row_stride % E == 0 && x_row_stride % E == 0 && dx_row_stride % E == 0 && g_batch_stride % E == 0 &&
+                     x_batch_stride % E == 0 && dx_batch_stride % E == 0,
+                 HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(grad_out) && hdcm_aligned16(x) && hdcm_aligned16(dx) && hdcm_aligned16(ln_w) &&
+                     hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w),
+                 HDCM_EALIGN);
+  if (B == 0 || L == 0) return HDCM_OK;
+  HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_norm_conv_bwd_workspace_bytes(B, L, D), HDCM_EWORKSPACE);
+  HDCM_CHECK_ARG(((uintptr_t)ws & 255u) == 0, HDCM_EALIGN);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HDCM_F32)
+    return launch_bwd<float>(grad_out, g_batch_stride, g_row_stride, x, x_batch_stride, x_row_stride, ln_w, ln_b,
+                             conv_w, dx, dx_batch_stride, dx_row_stride, d_ln_w, d_ln_b, d_conv_w, d_conv_b, ws, B,
+                             L, D, eps, s);
+  return launch_bwd<bf16_t>(grad_out, g_batch_stride, g_row_stride, x, x_batch_stride, x_row_stride, ln_w, ln_b,
+                            conv_w, dx, dx_batch_stride, dx_row_stride, d_ln_w, d_ln_b, d_conv_w, d_conv_b, ws, B, L,
+                            D, eps, s);
+}

@@ -46,20 +46,28 @@ class BlockState:
 
 
 class FusedNormConv1dFunction(torch.autograd.Function):
-    """LayerNorm + causal depthwise conv1d (width 4), forward on the HIP kernel.
+    """LayerNorm + causal depthwise conv1d (width 4) on the HIP kernels.
 
     Same ``apply(x, norm_weight, norm_bias, conv_weight[D,4], conv_bias, eps)`` signature
-    as hdcmamba/model.py:126-146.  Only the forward is built.
+    and backward outputs (dx and the four parameter gradients in x's dtype, None for eps)
+    as hdcmamba/model.py:126-166.  The backward is the exact gradient of the forward,
+    including the LayerNorm bias terms (also through the LayerNorm of the zero rows before
+    the sequence start) that the reference's backward kernel leaves out, from fp32 row
+    statistics.
     """
 
     @staticmethod
     def forward(ctx, x, norm_weight, norm_bias, conv_weight, conv_bias, eps):
+        ctx.save_for_backward(x, norm_weight, norm_bias, conv_weight)
+        ctx.eps = eps
         return _ops.norm_conv(x, norm_weight, norm_bias, conv_weight, conv_bias, eps)
 
     @staticmethod
     def backward(ctx, grad_output):
-        raise NotImplementedError("hdcmamba_amd builds the forward path only; "
-                                  "FusedNormConv1dFunction has no backward kernel")
+        x, norm_weight, norm_bias, conv_weight = ctx.saved_tensors
+        dx, dnw, dnb, dcw, dcb = _ops.norm_conv_bwd(grad_output, x, norm_weight, norm_bias, conv_weight, ctx.eps)
+        return (dx, dnw.to(x.dtype), dnb.to(x.dtype), dcw.to(x.dtype).view_as(conv_weight), dcb.to(x.dtype),
+                None)
 
 
 def fused_norm_conv1d_trainable(x, norm_layer, conv_layer):

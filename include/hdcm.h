@@ -61,6 +61,25 @@ int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t x_row_stri
                        int64_t B, int64_t L, int64_t D, float eps, int dtype, void* stream);
 
 /*
+ * Gradients of hdcm_norm_conv_fwd for grad_out = dL/dout [B,L,D] (strides as x): dx
+ * [B,L,D] in the activation dtype, and fp32 d_ln_w [D], d_ln_b [D], d_conv_w [D,4],
+ * d_conv_b [D].  Exact gradients of the forward, including the ln_b terms through the
+ * LayerNorm of the zero rows before the sequence start; parameter gradients are summed in
+ * a fixed order (deterministic).  ws: hdcm_norm_conv_bwd_workspace_bytes(B, L, D) bytes,
+ * 256-byte aligned.  Needs D/(16/elt_size) <= 256.
+ * Replaces: FusedNormConv1dFunction.backward -> _fused_norm_conv_bwd_kernel
+ *           (hdcmamba/model.py:149-166, kernel model.py:74-124), which omits the ln_b
+ *           terms of d_conv_w and d_ln_b and uses bf16-rounded row statistics.
+ */
+size_t hdcm_norm_conv_bwd_workspace_bytes(int64_t B, int64_t L, int64_t D);
+int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_row_stride,
+                       const void* x, int64_t x_batch_stride, int64_t x_row_stride, const void* ln_w,
+                       const void* ln_b, const void* conv_w, void* dx, int64_t dx_batch_stride,
+                       int64_t dx_row_stride, float* d_ln_w, float* d_ln_b, float* d_conv_w,
+                       float* d_conv_b, void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t D,
+                       float eps, int dtype, void* stream);
+
+/*
  * Diagonal selective scan over ds channels.  For row (b,t) of projs, columns
  * [0,ds) hold dt_raw, [ds,2ds) x and [2ds,3ds) b.  With dt = softplus(dt_raw)
  * (threshold 20) and A = -exp(A_log): h_t = h_{t-1} * exp(dt*A) + dt*b*x,

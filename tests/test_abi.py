@@ -156,6 +156,28 @@ def test_skinny_gemm_validation():
     assert f(*a) == OK
 
 
+def test_norm_conv_bwd_validation():
+    lib = _ops.lib()
+    assert lib.hdcm_norm_conv_bwd_workspace_bytes(1, 32768, 1024) == 32768 * 8 + 128 * 7 * 1024 * 4
+    assert lib.hdcm_norm_conv_bwd_workspace_bytes(0, 10, 64) == 0
+    # hdcm_norm_conv_bwd(go, g_bs, g_rs, x, x_bs, x_rs, ln_w, ln_b, conv_w, dx, d_bs, d_rs,
+    #                    d_ln_w, d_ln_b, d_conv_w, d_conv_b, ws, ws_bytes, B, L, D, eps, dtype, stream)
+    f = lib.hdcm_norm_conv_bwd
+    ws_n = lib.hdcm_norm_conv_bwd_workspace_bytes(2, 64, 256)
+    base = [P16, 64 * 256, 256, P16, 64 * 256, 256, P16, P16, P16, P16, 64 * 256, 256,
+            P16, P16, P16, P16, P16, ws_n, 2, 64, 256, 1e-5, 1, None]
+    a = list(base); a[12] = None  # no d_ln_w
+    assert f(*a) == EINVAL
+    a = list(base); a[17] = ws_n - 1  # short workspace
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[20] = 4096; a[2] = a[5] = a[11] = 4096; a[1] = a[4] = a[10] = 64 * 4096  # D too wide
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[20] = 250; a[2] = a[5] = a[11] = 250; a[1] = a[4] = a[10] = 64 * 250
+    assert f(*a) == EALIGN
+    a = list(base); a[18] = 0
+    assert f(*a) == OK
+
+
 def test_rowln_validation():
     f = _ops.lib().hdcm_rowln_fwd
     base = [P16, 1152, P16, 1152, None, None, 10, 1152, 1e-5, 1, None]

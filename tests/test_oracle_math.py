@@ -279,3 +279,52 @@ def test_stream_equals_sequential_recurrence(n_prefill):
     # continuation semantics are not a re-forward unless the grids agree
     if pad != 2:
         assert (oracle.block_forward(p, x, cfg) - got).abs().max() > 1e-4
+
+
+# ----------------------------------------------------------------------------- norm_conv gradients
+def _norm_conv_library(x, w, b, cw, cb, eps):
+    """LayerNorm then depthwise conv1d through PyTorch's own modules, the three rows before
+    the sequence start being the LayerNorm of a zero row (= b)."""
+    B, L, D = x.shape
+    u = torch.nn.functional.layer_norm(x, (D,), w, b, eps)
+    up = torch.cat([b.expand(B, 3, D), u], 1).transpose(1, 2)
+    return torch.nn.functional.conv1d(up, cw.unsqueeze(1), cb, groups=D).transpose(1, 2)
+
+
+def _grad_inputs(seed, B=2, L=7, D=16, beta=0.3):
+    g = torch.Generator().manual_seed(seed)
+    t = lambda *s, sc=1.0, off=0.0: (sc * torch.randn(*s, generator=g) + off).requires_grad_()
+    return [t(B, L, D, sc=2.0, off=0.5), t(D, sc=0.2, off=1.0), t(D, sc=beta), t(D, 4, sc=0.5), t(D, sc=0.1)]
+
+
+def test_norm_conv_gradients_equal_library_autograd():
+    """Gradients of the oracle's LN+conv (all five inputs) equal those PyTorch's layer_norm
+    and conv1d backward kernels give for the same forward, LN-bias halo included."""
+    ins = _grad_inputs(0)
+    go = torch.randn(2, 7, 16, generator=torch.Generator().manual_seed(1))
+    g_or = torch.autograd.grad(oracle.norm_conv(*ins, 1e-5), ins, go)
+    g_lib = torch.autograd.grad(_norm_conv_library(*ins, 1e-5), ins, go)
+    for a, b, name in zip(g_or, g_lib, ["x", "ln_w", "ln_b", "conv_w", "conv_b"]):
+        torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5, msg=name)
+
+
+def test_norm_conv_gradients_finite_differences():
+    """The oracle's gradients against central differences (fp32, step 1e-2)."""
+    ins = [t.detach().double().requires_grad_() for t in _grad_inputs(2, B=1, L=5, D=8)]
+    fn = lambda *a: oracle.norm_conv(*[t.float() for t in a], 1e-5).double()
+    assert torch.autograd.gradcheck(fn, ins, eps=1e-2, atol=2e-3, rtol=2e-3)
+
+
+def test_norm_conv_bias_gradient_includes_the_halo():
+    """d ln_b collects the conv taps that read the LayerNorm-of-zero rows before the start:
+    with a gradient on out[0] only, d ln_b = B (w0 + w1 + w2) from the three halo rows plus
+    B w3 from the b term of u[0].  A backward that drops the halo (as the reference kernel
+    does) gets B w3 only."""
+    ins = _grad_inputs(3)
+    go = torch.zeros(2, 7, 16)
+    go[:, 0] = 1.0  # only out[0] matters: u[-3], u[-2], u[-1] (= b) and u[0]
+    grads = torch.autograd.grad(oracle.norm_conv(*ins, 1e-5), ins, go)
+    cw = ins[3].detach()
+    # d out[0] / d b = sum of the three halo taps + the tap on u[0] (whose b term is 1)
+    want = 2 * (cw[:, 0] + cw[:, 1] + cw[:, 2] + cw[:, 3])
+    torch.testing.assert_close(grads[2], want, atol=1e-5, rtol=1e-5)
