@@ -39,6 +39,28 @@ def _cpu_model():
     return platform.processor() or "unknown"
 
 
+def forward_totals(cfg):
+    """Algorithmic FLOPs and compulsory HBM bytes of one LM forward (bf16, eb=2).
+
+    Per block, bytes: norm_conv (read x, write x_conv), in_proj (read x_conv and W, write
+    projs), SSM (read dt/x/b, write y), slot state pre-pass (read k, v), slot_gate (read
+    q/k/v/gate, write output), rowln (read and write combined), out_proj (read combined, W
+    and the residual, write the residual).  FLOPs: in_proj, out_proj and the slot
+    contractions (dense C x C count).  Plus embedding, the two final LayerNorms and the tied
+    head (read x and the embedding, write the logits)."""
+    eb = 2
+    T = cfg["B"] * cfg["L"]
+    dm, ds, H, C, V = cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"], 50304
+    hd, P = dm // H, 3 * ds + 4 * dm
+    blk_bytes = T * eb * (2 * dm + (dm + P) + 4 * ds + 2 * dm + 5 * dm + 2 * (ds + dm) + (ds + 3 * dm)) \
+        + eb * (P * dm + dm * (ds + dm))
+    blk_flops = 2 * T * dm * P + 2 * T * (ds + dm) * dm + T * H * (4 * C * hd + 4 * hd * hd)
+    n = cfg["n_layers"]
+    tail_bytes = T * eb * dm * (1 + 4 + 1) + V * dm * eb + T * V * eb
+    tail_flops = 2 * T * dm * V
+    return n * blk_flops + tail_flops, n * blk_bytes + tail_bytes
+
+
 def kernel_bytes(cfg, name):
     """Algorithmic HBM bytes per token of one launch of each custom kernel (bf16 eb=2)."""
     eb = 2 if cfg["dtype_name"] == "bf16" else 4
@@ -319,6 +341,15 @@ def main():
         kernels["slot_op(state+gate)"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
                                           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
+    forward_summary = None
+    if args.workload.startswith("lm"):
+        fl, by = forward_totals(cfg)
+        sec_step = ms_per_step * 1e-3
+        forward_summary = {"TFLOP": round(fl / 1e12, 2), "TFLOP/s": round(fl / sec_step / 1e12, 1),
+                           "frac_bf16_mfma_peak": round(fl / sec_step / 2.5e15, 4),
+                           "GB": round(by / 1e9, 2), "GB/s": round(by / sec_step / 1e9, 1),
+                           "frac_hbm_peak": round(by / sec_step / 8e12, 4)}
+
     cpu = None
     if args.cpu_baseline == "on" and args.workload.startswith("lm"):
         cpu = cpu_baseline(model, inp, cfg, args.cpu_budget_s)
@@ -336,6 +367,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "forward": forward_summary,
         "timing": {"steps": "HIP graph replays of the whole forward" if use_graph else "eager forwards",
                    "kernels": f"HIP events around each custom kernel over {k_steps} eager forwards",
                    "eager_ms_per_step": round(eager_ms, 3)},
