@@ -119,7 +119,6 @@ __global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
   }
 }
 
-__device__ __forceinline__ float phi_f(float z) { return fexp(fminf(z, 0.f)) + fmaxf(z, 0.f); }
 
 // grid (H + 1, B): x < H is head x's slot step, x == H the SSM channels of batch row b.
 // A slot workgroup owns one head's two fp32 states [HD][HD]; thread t holds 4 consecutive

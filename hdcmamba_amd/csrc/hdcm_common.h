@@ -130,6 +130,14 @@ __device__ __forceinline__ float quad_group_sum(float v) {
 }
 
 // softplus with the threshold 20 of F.softplus: x above it, log(1 + exp(x)) below.
+// Feature map elu(z)+1 of the slot memory: exp(min(z,0)) + max(z,0), which is z+1 for z>0
+// and exp(z) otherwise.  min and max against +0 are taken on the bit patterns as signed
+// integers (IEEE floats of either sign order like their patterns), so no canonicalising
+// v_max is needed on inputs that were bit-cast from bf16 storage.
+__device__ __forceinline__ float phi_f(float z) {
+  const int b = __float_as_int(z);
+  return fexp(__int_as_float(min(b, 0))) + __int_as_float(max(b, 0));
+}
 __device__ __forceinline__ float softplus20(float v) { return v > 20.0f ? v : flog(1.0f + fexp(v)); }
 
 // One Hillis-Steele step of the (a, u) scan: combine with the pair fetched by the DPP
@@ -206,11 +214,25 @@ __device__ __forceinline__ void frag_load4x2(Frag<float>& f, const float* p0, co
   f.v[0] = a.x; f.v[1] = a.y; f.v[2] = a.z; f.v[3] = a.w;
   f.v[4] = b.x; f.v[5] = b.y; f.v[6] = b.z; f.v[7] = b.w;
 }
-// Build a fragment from 8 fp32 values, rounding to the operand type.
-__device__ __forceinline__ void frag_from_f32(Frag<bf16_t>& f, const float* x) {
-#pragma unroll
-  for (int s = 0; s < 8; ++s) f.v[s] = (__bf16)x[s];
+// 8 fp32 values rounded (nearest even) into 8 bf16: four paired v_cvt_pk_bf16_f32.
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* x) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]),
+                   pack_bf16x2(x[6], x[7])};
+  return __builtin_bit_cast(bf16x8_t, u);
 }
+// The 8 values of a bf16 vector as fp32 (exact).
+__device__ __forceinline__ void unpack_bf16x8(bf16x8_t v, float* x) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = __uint_as_float(u[i] << 16);
+    x[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+// Build a fragment from 8 fp32 values, rounding to the operand type.
+__device__ __forceinline__ void frag_from_f32(Frag<bf16_t>& f, const float* x) { f.v = pack_bf16x8(x); }
 __device__ __forceinline__ void frag_from_f32(Frag<float>& f, const float* x) {
 #pragma unroll
   for (int s = 0; s < 8; ++s) f.v[s] = x[s];

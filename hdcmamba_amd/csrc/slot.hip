@@ -118,9 +118,6 @@ __device__ __forceinline__ void frag_tok(Frag<T>& f, const T* tile, int d0, int 
   }
 }
 
-// elu(z)+1 without a branch or select: exp(min(z,0)) + max(z,0) is exp(z) for z<=0 and
-// 1+z for z>0.
-__device__ __forceinline__ float phi_f(float z) { return fexp(fminf(z, 0.f)) + fmaxf(z, 0.f); }
 
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float* v);
@@ -130,10 +127,7 @@ __device__ __forceinline__ void store4<float>(float* p, const float* v) {
 }
 template <>
 __device__ __forceinline__ void store4<bf16_t>(bf16_t* p, const float* v) {
-  uint2 u;
-  u.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-  u.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-  *reinterpret_cast<uint2*>(p) = u;
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
 // 4 consecutive elements from global memory as fp32.
@@ -167,9 +161,12 @@ __device__ __forceinline__ bf16_t raw_elem<bf16_t>(const uint4& v, int e) {
 
 // Scale the 8 slots of a fragment by c, rounding to the operand type.
 __device__ __forceinline__ Frag<bf16_t> frag_scale(const Frag<bf16_t>& f, float c) {
-  Frag<bf16_t> o;
+  float x[8];
+  unpack_bf16x8(f.v, x);
 #pragma unroll
-  for (int s = 0; s < 8; ++s) o.v[s] = (__bf16)((float)f.v[s] * c);
+  for (int s = 0; s < 8; ++s) x[s] *= c;
+  Frag<bf16_t> o;
+  o.v = pack_bf16x8(x);
   return o;
 }
 __device__ __forceinline__ Frag<float> frag_scale(const Frag<float>& f, float c) {
@@ -263,11 +260,17 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
       unpack16<T>(raw[it], f);
       const float kd = ok ? fexp2((float)(tlen - 1 - i) * lg2) : 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        f[e] = ok ? rnd<T>(phi_f(f[e])) : 0.f;
-        kdv[e] = f[e] * kd;
+      for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
+      if constexpr (sizeof(T) == 2) {
+        // round phi(k) once, in pairs; the rounded words are stored as they are
+        const bf16x8_t pk = pack_bf16x8(f);
+        if (!STATE_ONLY) *reinterpret_cast<bf16x8_t*>(sm + LD::oK + i * LD::PQ + cg * E) = pk;
+        unpack_bf16x8(pk, f);
+      } else {
+        if (!STATE_ONLY) store16<T>(sm + LD::oK + i * LD::PQ + cg * E, f);
       }
-      if (!STATE_ONLY) store16<T>(sm + LD::oK + i * LD::PQ + cg * E, f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) kdv[e] = f[e] * kd;
       if constexpr (LD::TR) {
         store16<T>(sKd + i * LD::PV + cg * E, kdv);
       } else {

@@ -114,3 +114,48 @@ def test_forward_graph_replays_match_eager(dev):
         assert max_rel(got, want) < 1e-3
     with pytest.raises(RuntimeError):
         fg(ids[0][:, :100])
+
+
+@pytest.mark.parametrize("name", ["lm_c3", "lm_c4"])
+def test_block_at_lm_shape(dev, name):
+    """One block at the full shape of the 12-layer (d_model 768, 12 heads, B=8, L=4096) and
+    the 24-layer long-context (d_model 1024, d_state 128, 16 heads, B=1, L=32768) models,
+    with decays drawn from U[0.9, 0.999] so the scan and slot carries span many chunks."""
+    from hdcmamba_amd import HdcMamba9v3Block
+    from cfgs import reinit_block_
+
+    cfg = WORKLOADS[name]
+    print("block at", name, cfg["B"], cfg["L"], cfg["d_model"], flush=True)
+    torch.manual_seed(11)
+    blk = HdcMamba9v3Block(cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"])
+    blk = reinit_block_(blk, seed=11, decays_uniform=True).eval().to(torch.bfloat16)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(cfg["B"], cfg["L"], cfg["d_model"], generator=g).to(torch.bfloat16)
+    ref = oracle.block_forward(_sd(blk), x, oracle_cfg(blk))
+    with torch.no_grad():
+        y, _ = blk.to(dev)(x.to(dev))
+    print("max rel", max_rel(y, ref), flush=True)
+    assert_close(y, ref, torch.bfloat16, name)
+
+
+def test_model_two_layers_long_context(dev):
+    """Two layers of the long-context model (d_model 1024, d_state 128, 16 heads) over one
+    sequence of 32768 tokens: residual stream, per-block norms and the final norm."""
+    from hdcmamba_amd import HdcMamba9v3Model
+    from cfgs import reinit_block_
+
+    cfg = WORKLOADS["lm_c4"]
+    print("model 2 layers", cfg["L"], flush=True)
+    torch.manual_seed(13)
+    m = HdcMamba9v3Model(cfg["d_model"], 2, cfg["d_state"], cfg["chunk"], num_heads=cfg["num_heads"],
+                         chunk_size=cfg["chunk"])
+    for i, blk in enumerate(m.layers):
+        reinit_block_(blk, seed=20 + i, decays_uniform=True)
+    m = m.eval().to(torch.bfloat16)
+    x = torch.randn(1, cfg["L"], cfg["d_model"], generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
+    ref = oracle.model_forward(_sd(m), x, oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"],
+                                                          cfg["chunk"]), 2)
+    with torch.no_grad():
+        y = m.to(dev)(x.to(dev))
+    print("max rel", max_rel(y, ref), flush=True)
+    assert_close_normwise(y, ref, torch.bfloat16, "2-layer model L=32768")
