@@ -298,7 +298,7 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
     stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, false>(raw, sm, tlen, lg2, tid);
 }
 
-template <typename T, int HD, int TC, bool HAS_W>
+template <typename T, int HD, int TC, bool HAS_W, bool PAIRS>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int dm, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
@@ -353,19 +353,27 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   uint4 raw[TL::NL];
   loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
 
-  // Gate values of this lane's output positions (row 16*w + l16 of a tile, columns
-  // 16*vt + 4*kg .. +3), kept as stored.  They are loaded one tile ahead, right after the
-  // current tile's outputs, so the load overlaps the state update, the next tile's
-  // staging and both barriers.  Rows past the tile read the tile's first row (never
-  // stored), which keeps the load count fixed and the memory-counter waits exact.
-  typedef typename std::conditional<sizeof(T) == 2, uint2, float4>::type G4;
-  G4 graw[NVT];
+  // Gate values of this lane's output positions (row 16*w + l16 of a tile), kept as
+  // stored.  They are loaded one tile ahead, right after the current tile's outputs, so
+  // the load overlaps the state update, the next tile's staging and both barriers.  Rows
+  // past the tile read the tile's first row (never stored), which keeps the load count
+  // fixed and the memory-counter waits exact.
+  //   fp32: columns 16*vt + 4*kg .. +3 of every 16-column tile vt (16 bytes each).
+  //   bf16 with 16-byte aligned output rows (PAIRS): 16-byte runs in the exchanged layout
+  //   of the output stage below: for each pair of tiles, columns
+  //   32*pp + 16*(kg&1) + 8*(kg>>1) .. +7.  Otherwise as fp32 (8 bytes each).
+  constexpr bool kPairs = PAIRS && sizeof(T) == 2;
+  constexpr int NG = kPairs ? NVT / 2 : NVT;
+  static_assert(!kPairs || NVT % 2 == 0, "tile pairs");
+  const int gcol = kPairs ? 16 * (kg & 1) + 8 * (kg >> 1) : 4 * kg;
+  const int gstep = kPairs ? 32 : 16;
+  uint4 graw[NG];
   const int giq = (w < NIT ? w : 0) * 16 + l16;
   auto load_gate = [&](int pt) {
     const int tl = min(TC, L - pt);
-    const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * prs + kg * 4;
+    const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * prs + gcol;
 #pragma unroll
-    for (int vt = 0; vt < NVT; ++vt) graw[vt] = *reinterpret_cast<const G4*>(grow + vt * 16);
+    for (int g = 0; g < NG; ++g) graw[g] = *reinterpret_cast<const uint4*>(grow + g * gstep);
   };
   if (w < NIT) load_gate(p_begin);
 
@@ -486,7 +494,42 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           sq += d * d;
         }
       const float rinv = rsqrtf(quad_group_sum(sq) * (1.0f / HD) + gn_eps);
-      if (iq < tlen) {
+      if constexpr (kPairs) {
+        // Tiles vt = 2pp and 2pp+1 leave this lane 4+4 values of row iq; one
+        // v_permlane16_swap per packed word trades them between the lane pairs (kg, kg^1) of
+        // the same row so that every lane ends with 8 consecutive columns (kg=0: tile 2pp
+        // cols 0-7, kg=1: tile 2pp+1 cols 0-7, kg=2: tile 2pp cols 8-15, kg=3: tile 2pp+1
+        // cols 8-15).  The gate arrives in that layout and is traded back the same way
+        // (the swap is its own inverse), so loads and stores are 16-byte runs and a row's
+        // 4 lanes cover 64 contiguous bytes.
+        T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + gcol;
+#pragma unroll
+        for (int pp = 0; pp < NG; ++pp) {
+          const uint4 gr = graw[pp];
+          const auto g0 = __builtin_amdgcn_permlane16_swap(gr.x, gr.z, false, false);
+          const auto g1 = __builtin_amdgcn_permlane16_swap(gr.y, gr.w, false, false);
+          const uint32_t gw[2][2] = {{g0[0], g1[0]}, {g0[1], g1[1]}};  // [tile of the pair][word]
+          uint32_t ow[2][2];
+#pragma unroll
+          for (int hv = 0; hv < 2; ++hv) {
+            const int vt = 2 * pp + hv;
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int dv = vt * 16 + kg * 4 + r;
+              const uint32_t gwr = gw[hv][r >> 1];
+              const float gv = __uint_as_float((r & 1) ? (gwr & 0xffff0000u) : (gwr << 16));
+              const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
+              o[r] = yn * frcp(1.0f + fexp(-gv));
+            }
+            ow[hv][0] = pack_bf16x2(o[0], o[1]);
+            ow[hv][1] = pack_bf16x2(o[2], o[3]);
+          }
+          const auto s0 = __builtin_amdgcn_permlane16_swap(ow[0][0], ow[1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane16_swap(ow[0][1], ow[1][1], false, false);
+          if (iq < tlen) *reinterpret_cast<uint4*>(orow + pp * 32) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+        }
+      } else if (iq < tlen) {
         T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + kg * 4;
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
@@ -767,16 +810,20 @@ int launch_gate(const void* projs, int64_t prs, int64_t q_col, const void* gamma
   const float* Ain = (const float*)ws + (size_t)B * H * pl.nseg * HD * HD;
   // heads vary fastest so the workgroups that run together read the same rows of projs
   dim3 grid((unsigned)H, pl.nseg, (unsigned)B);
-  if (pl.has_w)
-    hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, true>), grid, dim3(kThreads), 0, s,
-                       (const T*)projs, prs, (int)q_col, (int)dm, (int)L, (int)C, pl.cshift,
-                       (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles,
-                       pl.nseg, (T*)out, ors, (int)out_col, S_final);
-  else
-    hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, false>), grid, dim3(kThreads), 0, s,
-                       (const T*)projs, prs, (int)q_col, (int)dm, (int)L, (int)C, pl.cshift,
-                       (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles,
-                       pl.nseg, (T*)out, ors, (int)out_col, S_final);
+  // 16-byte output runs need 16-byte aligned rows and columns (bf16 only; fp32 always has them)
+  const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0;
+#define HDCM_GATE_LAUNCH(W, P)                                                                         \
+  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P>), grid, dim3(kThreads), 0, s, (const T*)projs, prs, \
+                     (int)q_col, (int)dm, (int)L, (int)C, pl.cshift, (const T*)gamma, (const T*)gn_w,       \
+                     (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, pl.nseg, (T*)out, ors, (int)out_col, S_final)
+  if (pl.has_w) {
+    if (pairs) HDCM_GATE_LAUNCH(true, true);
+    else HDCM_GATE_LAUNCH(true, false);
+  } else {
+    if (pairs) HDCM_GATE_LAUNCH(false, true);
+    else HDCM_GATE_LAUNCH(false, false);
+  }
+#undef HDCM_GATE_LAUNCH
   return hdcm_launch_status();
 }
 

@@ -110,6 +110,7 @@ SLOT_CASES = [
     (torch.bfloat16, 1, 256, 768, 8, 64),    # hd 96
     (torch.bfloat16, 1, 512, 512, 8, 32),
     (torch.bfloat16, 1, 512, 512, 8, 256),
+    (torch.bfloat16, 2, 96, 256, 4, 32),     # last row tile half full (32 of 64 rows)
 ]
 
 
@@ -137,6 +138,25 @@ def test_slot_gate(dev, dtype, B, L, dm, H, C):
     assert_close(out[..., ds:], ref, dtype, "slot+gate")
     assert out[..., :ds].abs().max().item() == 0.0
     assert_close(sf / S.abs().max(), S / S.abs().max(), dtype, "slot S_final")
+
+
+@pytest.mark.parametrize("out_col", [4, 8])
+def test_slot_gate_output_alignment(dev, out_col):
+    """bf16 outputs whose rows are only 8-byte aligned take the 8-byte store path; 16-byte
+    aligned ones the exchanged 16-byte path.  Both match the oracle."""
+    _say("slot_gate out_col", out_col)
+    dm, ds, H, C, B, L = 512, 64, 8, 64, 1, 320
+    dtype = torch.bfloat16
+    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, dtype, seed=out_col)
+    pd = projs.to(dev)
+    out = torch.zeros(B, L, out_col + dm, device=dev, dtype=dtype)
+    ws = _ops.slot_workspace(pd, dm, H, C)
+    _ops.slot_state(pd, 3 * ds, gamma.to(dev), dm, H, C, ws)
+    _ops.slot_gate(pd, 3 * ds, gamma.to(dev), gn_w.to(dev), gn_b.to(dev), 1e-5, ws, out, out_col, dm, H, C)
+    y, _ = oracle.slot_chunked(projs, gamma, dm, ds, H, C, dtype)
+    ref = oracle.gnorm_gate(y, projs[..., 3 * ds + 3 * dm:], gn_w, gn_b, H).to(dtype)
+    assert_close(out[..., out_col:], ref, dtype, f"slot+gate out_col={out_col}")
+    assert out[..., :out_col].abs().max().item() == 0.0
 
 
 def test_slot_segments_env(dev, monkeypatch):
