@@ -76,6 +76,102 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
   }
 }
 
+// Wide outputs (N >= kWideN): a workgroup of 8 waves per 16 output columns, each wave owning a
+// contiguous K range of the 16 weight rows.  A wave reads its range row by row (lane i of
+// load instruction j takes 16-byte piece 64*j + i of the range, row-major), so one instruction
+// covers about two rows with a few hundred contiguous bytes each instead of 16 rows x 64
+// bytes, and stages it in a private LDS slab, from which the B fragments are read.  Every
+// lane issues the same number of loads (pieces past the wave's range re-read one inside the
+// row and are never used), so all loads are in flight before the first wait.
+constexpr int kLdsWaves = 8;
+constexpr int kLdsThreads = kLdsWaves * kWave;
+constexpr int kWideN = 2048;
+
+template <int STEPS, bool BIAS, bool RES>
+__global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
+    const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
+    const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
+    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K) {
+  constexpr int PITCH = STEPS * 32 + 8;  // slab row pitch (elements): +16 bytes staggers the banks
+  __shared__ __attribute__((aligned(16))) bf16_t slab[kLdsWaves][16 * PITCH];
+  __shared__ float part[kLdsWaves][16][17];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nsteps = K / 32;
+  const int base = nsteps / kLdsWaves, extra = nsteps % kLdsWaves;
+  const int my = base + (w < extra ? 1 : 0);
+  const int s0 = w * base + (w < extra ? w : extra);
+  // the K step a slot s < STEPS of this wave reads: its own, or (past its range) one inside the row
+  auto step_of = [&](int s) { return min(s0 + max(min(s, my - 1), 0), nsteps - 1); };
+
+  uint4 raw[STEPS];
+#pragma unroll
+  for (int i = 0; i < STEPS; ++i) {
+    const int idx = kWave * i + lane;
+    const int r = idx / (4 * STEPS), s = (idx / 4) % STEPS, q = idx % 4;
+    const int n = min(n0 + r, N - 1);  // rows past N re-read row N-1 (outputs not stored)
+    raw[i] = *reinterpret_cast<const uint4*>(W + (int64_t)n * w_rs + 32 * step_of(s) + 8 * q);
+  }
+  const int am = l16 < M ? l16 : 0;  // rows past M read row 0 (outputs not stored)
+  Frag<bf16_t> fa[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+    fa[s].v = *reinterpret_cast<const bf16x8_t*>(A + (int64_t)am * a_rs + 32 * step_of(s) + 8 * g);
+  bf16_t* sl = slab[w];
+#pragma unroll
+  for (int i = 0; i < STEPS; ++i) {
+    const int idx = kWave * i + lane;
+    const int r = idx / (4 * STEPS), s = (idx / 4) % STEPS, q = idx % 4;
+    *reinterpret_cast<uint4*>(sl + r * PITCH + 32 * s + 8 * q) = raw[i];
+  }
+  __syncthreads();
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    if (s < my) {
+      Frag<bf16_t> b;
+      b.v = *reinterpret_cast<const bf16x8_t*>(sl + l16 * PITCH + 32 * s + 8 * g);
+      acc = mma(fa[s], b, acc);
+    }
+  }
+  // D layout: lane holds D[4 g + r][l16]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
+  __syncthreads();
+  if (tid < 256) {
+    const int m = tid / 16, nn = tid % 16, n = n0 + nn;
+    float v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kLdsWaves; ++k) v += part[k][m][nn];
+    if (m < M && n < N) {
+      if (BIAS) v += bf2f(bias[n]);
+      if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
+      out[(int64_t)m * o_rs + n] = f2bf(v);
+    }
+  }
+}
+
+template <int STEPS>
+void launch_lds(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
+                int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
+  bf16_t* o = (bf16_t*)out;
+  if (bias && res)
+    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, true, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K);
+  else if (bias)
+    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, true, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K);
+  else if (res)
+    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K);
+  else
+    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
+                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K);
+}
+
 template <int STEPS>
 void launch_steps(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
                   int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
@@ -113,8 +209,20 @@ extern "C" int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const v
                  HDCM_EALIGN);
   if (M == 0 || N == 0) return HDCM_OK;
   hipStream_t s = (hipStream_t)stream;
-  const int steps = (int)((K / 32 + kWaves - 1) / kWaves);
   const int m = (int)M, n = (int)N, k = (int)K;
+  if (N >= kWideN) {
+    const int lsteps = (int)((K / 32 + kLdsWaves - 1) / kLdsWaves);  // <= 12 since K <= 3072
+    if (lsteps <= 4)
+      launch_lds<4>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+    else if (lsteps <= 8)
+      launch_lds<8>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+    else if (lsteps <= 9)
+      launch_lds<9>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+    else
+      launch_lds<12>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
+    return hdcm_launch_status();
+  }
+  const int steps = (int)((K / 32 + kWaves - 1) / kWaves);
   if (steps <= 8)
     launch_steps<8>(A, a_row_stride, W, w_row_stride, bias, res, res_row_stride, out, out_row_stride, m, n, k, s);
   else if (steps <= 12)

@@ -186,6 +186,10 @@ def test_slot_unsupported_head_dim(dev):
     (16, 768, 832, False, True),
     (1, 100, 64, True, True),
     (5, 33, 3072, False, False),
+    # N >= 2048 runs the LDS-staged kernel: fewer K steps than waves, ragged N, K = 3072
+    (3, 2048, 64, True, True),
+    (9, 2050, 1024, False, True),
+    (16, 4096, 3072, True, False),
 ])
 def test_skinny_gemm(dev, M, N, K, bias, res):
     """bf16 operands, fp32 accumulation, one rounding: against torch fp32 on the same
