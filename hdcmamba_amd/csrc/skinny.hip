@@ -5,13 +5,15 @@
 // hdcmamba/model.py:313,325,340,383 and train_fineweb.py:55,94 run them as nn.Linear).
 //
 // At M = 16 every weight is read once per step and used for 16 rows only, so the GEMM is
-// bound by streaming W from HBM.  A workgroup of four waves owns one 16-column tile of
-// the output; its waves split K four ways and each issues all of its W loads (one 16-byte
-// fragment per lane per K=32 step, 16 rows x 64 contiguous bytes per instruction) before
-// the first v_mfma_f32_16x16x32_bf16, so a wave keeps its whole share of W in flight.  A
-// (the 16 activation rows, a few tens of KB) is read from L2 the same way.  The four partial
-// 16x16 tiles are summed through LDS and the epilogue adds bias and residual in fp32 and
-// rounds once to bf16.
+// bound by streaming W from HBM.  Two kernels, both with one workgroup per 16-column tile
+// of the output and every load of a wave issued before its first v_mfma_f32_16x16x32_bf16:
+//   skinny_gemm_kernel: four waves split K four ways; each lane loads its MFMA fragments
+//     straight from W (16 rows x 64 contiguous bytes per instruction).
+//   skinny_lds_kernel (N >= 2048, where it is faster): eight waves split K eight ways; a
+//     wave reads its K range of the 16 rows row-major (a few hundred contiguous bytes of a
+//     row per instruction) into a private LDS slab and takes the fragments from there.
+// A (the 16 activation rows, a few tens of KB) is read from L2.  The partial 16x16 tiles are
+// summed through LDS and the epilogue adds bias and residual in fp32 and rounds once to bf16.
 #include "hdcm_common.h"
 
 using namespace hdcm;
