@@ -65,24 +65,40 @@ __global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
   // rows 0..2: history (oldest first), row 3: the new token
   const T* rows[4] = {hist + ((int64_t)b * 3 + 0) * D, hist + ((int64_t)b * 3 + 1) * D,
                       hist + ((int64_t)b * 3 + 2) * D, x + (int64_t)b * x_rs};
+  // Every load of the step is issued up front: the four rows, then the LayerNorm and conv
+  // parameters (kept as stored until after the statistics), so one memory round trip
+  // covers the whole step.  Groups past G read group 0 (their results are not stored).
+  uint4 raw[4][NG], prm[7][NG];
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = tid + kThreads * i < G ? tid + kThreads * i : 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) raw[k][i] = ldg16(rows[k] + g * E);
+  }
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = tid + kThreads * i < G ? tid + kThreads * i : 0;
+    prm[0][i] = ldg16(ln_w + g * E);
+    prm[1][i] = ldg16(ln_b + g * E);
+    prm[2][i] = ldg16(conv_b + g * E);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) prm[3 + k][i] = ldg16(conv_w + (int64_t)g * E * 4 + k * E);
+  }
   float r[4][NG][E];
   float st[8];
 #pragma unroll
   for (int n = 0; n < 8; ++n) st[n] = 0.f;
 #pragma unroll
   for (int i = 0; i < NG; ++i) {
-    const int g = tid + kThreads * i;
+    const bool ok = tid + kThreads * i < G;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      if (g < G) load16<T>(rows[k] + g * E, r[k][i]);
-      else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) r[k][i][e] = 0.f;
-      }
+      unpack16<T>(raw[k][i], r[k][i]);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        st[2 * k] += r[k][i][e];
-        st[2 * k + 1] += r[k][i][e] * r[k][i][e];
+        const float v = ok ? r[k][i][e] : 0.f;
+        st[2 * k] += v;
+        st[2 * k + 1] += v * v;
       }
     }
   }
@@ -100,11 +116,11 @@ __global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
     const int g = tid + kThreads * i;
     if (g >= G) continue;
     float w[E], bb[E], cb[E], cw[4 * E], o[E];
-    load16<T>(ln_w + g * E, w);
-    load16<T>(ln_b + g * E, bb);
-    load16<T>(conv_b + g * E, cb);
+    unpack16<T>(prm[0][i], w);
+    unpack16<T>(prm[1][i], bb);
+    unpack16<T>(prm[2][i], cb);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)g * E * 4 + k * E, cw + k * E);
+    for (int k = 0; k < 4; ++k) unpack16<T>(prm[3 + k][i], cw + k * E);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       float acc = cb[e];
@@ -115,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void norm_conv_step_kernel(
     store16<T>(out + (int64_t)b * o_rs + g * E, o);
     // shift the history: rows 1, 2 and the new token become rows 0, 1, 2
 #pragma unroll
-    for (int k = 0; k < 3; ++k) store16<T>(hist + ((int64_t)b * 3 + k) * D + g * E, r[k + 1][i]);
+    for (int k = 0; k < 3; ++k) *reinterpret_cast<uint4*>(hist + ((int64_t)b * 3 + k) * D + g * E) = raw[k + 1][i];
   }
 }
 
@@ -167,6 +183,14 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
       sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
       si[k] = *reinterpret_cast<const float4*>(S_intra + sbase + (int64_t)i * HD);
     }
+  }
+  // this thread's gate and GroupNorm parameters, loaded with the states (used last)
+  T gate_raw = T(), gnw_raw = T(), gnb_raw = T();
+  if (tid < HD) {
+    const int col = h * HD + tid;
+    gate_raw = row[q_col + 3 * dm + col];
+    gnw_raw = gn_w[col];
+    gnb_raw = gn_b[col];
   }
   // chunk offset: from device memory when the step runs inside a captured graph
   const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
@@ -224,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   const float rinv = rsqrtf(var + gn_eps);
   if (tid < HD) {
     const int col = h * HD + tid;
-    const float gate = to_f<T>(row[q_col + 3 * dm + col]);
-    const float yn = (y - mean) * rinv * to_f<T>(gn_w[col]) + to_f<T>(gn_b[col]);
+    const float gate = to_f<T>(gate_raw);
+    const float yn = (y - mean) * rinv * to_f<T>(gnw_raw) + to_f<T>(gnb_raw);
     orow[g_col + col] = from_f<T>(yn * frcp(1.0f + fexp(-gate)));
   }
 }
