@@ -47,6 +47,9 @@ _PROTOS = {
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
     "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                      c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_rowln_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "hdcm_rowln_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+                               c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_float, c_int, c_void_p]),
     "hdcm_norm_conv_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "hdcm_norm_conv_bwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
                                    c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
@@ -297,6 +300,31 @@ def layer_norm(x, w=None, b=None, eps=1e-5, out=None):
         rows, W, float(eps), _dtype(x), _stream(x)))
     timer.end("rowln", ev)
     return out
+
+
+def layer_norm_bwd(grad_out, x, w=None, eps=1e-5):
+    """Gradient of layer_norm: (dx in x.dtype, dw fp32 or None, db fp32 or None)."""
+    _on_gpu(grad_out, x)
+    W = x.shape[-1]
+    if grad_out.shape != x.shape or grad_out.dtype != x.dtype:
+        raise RuntimeError("layer_norm_bwd: grad_out must match x in shape and dtype")
+    grad_out, x = grad_out.contiguous(), x.contiguous()
+    rows = x.numel() // W if W else 0
+    dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    dw = db = ws = None
+    if w is not None:
+        w = _same(w, x, "w")
+        dw = torch.empty(W, device=x.device, dtype=torch.float32)
+        db = torch.empty(W, device=x.device, dtype=torch.float32)
+        ws = torch.empty(max(lib().hdcm_rowln_bwd_workspace_bytes(rows, W), 16), dtype=torch.uint8,
+                         device=x.device)
+    _check("hdcm_rowln_bwd", lib().hdcm_rowln_bwd(
+        grad_out.data_ptr(), _rows2d(grad_out, "grad_out"), x.data_ptr(), _rows2d(x, "x"),
+        w.data_ptr() if w is not None else None, dx.data_ptr(), _rows2d(dx, "dx"),
+        dw.data_ptr() if dw is not None else None, db.data_ptr() if db is not None else None,
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, rows, W, float(eps),
+        _dtype(x), _stream(x)))
+    return dx, dw, db
 
 
 # ----------------------------------------------------------------------------- decode step

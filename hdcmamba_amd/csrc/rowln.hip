@@ -146,7 +146,7 @@ extern "C" int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out,
                               int64_t out_row_stride, const void* w, const void* b, int64_t rows,
                               int64_t width, float eps, int dtype, void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(in && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG((in && out) || rows == 0, HDCM_EINVAL);  // empty inputs may have no storage
   HDCM_CHECK_ARG((w == nullptr) == (b == nullptr), HDCM_EINVAL);
   HDCM_CHECK_ARG(rows >= 0 && width > 0, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
@@ -162,4 +162,224 @@ extern "C" int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out,
   if (dtype == HDCM_F32)
     return launch<float>(in, in_row_stride, out, out_row_stride, w, b, rows, width, eps, s);
   return launch<bf16_t>(in, in_row_stride, out, out_row_stride, w, b, rows, width, eps, s);
+}
+
+// ------------------------------------------------------------------------- backward
+// Gradient of the row LayerNorm above (nn.LayerNorm's backward, as autograd runs it for
+// the reference's norm_final / F.layer_norm at hdcmamba/model.py:382,404):
+//   x^ = (x - mean) * rstd,  g = dy * w (or dy without affine)
+//   dx = rstd * (g - mean(g) - x^ * mean(g * x^))
+//   dw = sum over rows of dy * x^,  db = sum over rows of dy
+// The statistics are recomputed from x in fp32.  Pass 1 (one wave per row, a fixed grid of
+// workgroups striding over the rows) writes dx and, with affine, each workgroup's column
+// sums of dy*x^ and dy; pass 2 adds those partials in a fixed order, so dw and db are
+// deterministic.
+namespace {
+
+constexpr int kBwdWaves = 4;
+constexpr int kBwdMaxBlocks = 1024;
+
+int64_t bwd_blocks(int64_t rows) {
+  const int64_t need = (rows + kBwdWaves - 1) / kBwdWaves;
+  return need < kBwdMaxBlocks ? (need > 0 ? need : 1) : kBwdMaxBlocks;
+}
+
+template <typename T, int NG, bool AFFINE>
+__global__ __launch_bounds__(kBwdWaves* kWave) void rowln_bwd_rows_kernel(
+    const T* __restrict__ dy, int64_t dy_rs, const T* __restrict__ x, int64_t x_rs,
+    const T* __restrict__ w, T* __restrict__ dx, int64_t dx_rs, float* __restrict__ part,
+    int64_t rows, int W, float eps) {
+  constexpr int E = Vec<T>::N;
+  __shared__ float red[AFFINE ? 2 : 1][AFFINE ? NG * E * kWave : 1];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int G = W / E;
+  const float invW = 1.0f / (float)W;
+  float ww[NG][E];
+  float adw[NG][E], adb[NG][E];
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = lane + kWave * i;
+#pragma unroll
+    for (int e = 0; e < E; ++e) ww[i][e] = 1.f, adw[i][e] = 0.f, adb[i][e] = 0.f;
+    if (AFFINE && g < G) load16<T>(w + (int64_t)g * E, ww[i]);
+  }
+  const int64_t stride = (int64_t)gridDim.x * kBwdWaves;
+  for (int64_t row = (int64_t)blockIdx.x * kBwdWaves + wave; row < rows; row += stride) {
+    uint4 rx[NG], rd[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int g = lane + kWave * i < G ? lane + kWave * i : 0;
+      rx[i] = ldg16(x + row * x_rs + (int64_t)g * E);
+      rd[i] = ldg16(dy + row * dy_rs + (int64_t)g * E);
+    }
+    float xv[NG][E], gv[NG][E];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const bool ok = lane + kWave * i < G;
+      unpack16<T>(rx[i], xv[i]);
+      unpack16<T>(rd[i], gv[i]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        if (!ok) xv[i][e] = 0.f, gv[i][e] = 0.f;
+        s += xv[i][e];
+      }
+    }
+    const float mean = wave_total(s) * invW;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const bool ok = lane + kWave * i < G;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float c = ok ? xv[i][e] - mean : 0.f;
+        xv[i][e] = c;
+        q += c * c;
+      }
+    }
+    const float rstd = rsqrtf(wave_total(q) * invW + eps);
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float xh = xv[i][e] * rstd;  // x^ (0 past W)
+        xv[i][e] = xh;
+        if (AFFINE) {
+          adw[i][e] += gv[i][e] * xh;
+          adb[i][e] += gv[i][e];
+        }
+        const float g = gv[i][e] * ww[i][e];
+        gv[i][e] = g;
+        sg += g;
+        sgx += g * xh;
+      }
+    const float mg = wave_total(sg) * invW, mgx = wave_total(sgx) * invW;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int g = lane + kWave * i;
+      if (g >= G) continue;
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = rstd * (gv[i][e] - mg - xv[i][e] * mgx);
+      store16<T>(dx + row * dx_rs + (int64_t)g * E, o);
+    }
+  }
+  if constexpr (AFFINE) {
+    // this workgroup's column sums: the waves add theirs into LDS in turn (wave order,
+    // deterministic), then one row of partials per workgroup
+    for (int k = 0; k < kBwdWaves; ++k) {
+      if (wave == k) {
+#pragma unroll
+        for (int i = 0; i < NG; ++i)
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const int slot = (i * kWave + lane) * E + e;  // column (lane + 64 i) * E + e
+            red[0][slot] = (k ? red[0][slot] : 0.f) + adw[i][e];
+            red[1][slot] = (k ? red[1][slot] : 0.f) + adb[i][e];
+          }
+      }
+      __syncthreads();
+    }
+    float* pw = part + (int64_t)blockIdx.x * 2 * W;
+    for (int c = threadIdx.x; c < G * E; c += kBwdWaves * kWave) {
+      pw[c] = red[0][c];
+      pw[W + c] = red[1][c];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rowln_bwd_reduce_kernel(const float* __restrict__ part, int nblk, int W,
+                                                               float* __restrict__ dw, float* __restrict__ db) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= W) return;
+  float a = 0.f, b = 0.f;
+  for (int k = 0; k < nblk; ++k) {
+    a += part[(int64_t)k * 2 * W + c];
+    b += part[(int64_t)k * 2 * W + W + c];
+  }
+  dw[c] = a;
+  db[c] = b;
+}
+
+template <typename T, int NG>
+int launch_bwd_ng(const void* dy, int64_t dy_rs, const void* x, int64_t x_rs, const void* w, void* dx,
+                  int64_t dx_rs, float* dw, float* db, float* ws, int64_t rows, int W, float eps, hipStream_t s) {
+  const int64_t nb = bwd_blocks(rows);
+  if (w) {
+    hipLaunchKernelGGL((rowln_bwd_rows_kernel<T, NG, true>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
+                       (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)w, (T*)dx, dx_rs, ws, rows, W, eps);
+    int st = hdcm_launch_status();
+    if (st) return st;
+    hipLaunchKernelGGL(rowln_bwd_reduce_kernel, dim3((unsigned)((W + 255) / 256)), dim3(256), 0, s, ws, (int)nb, W,
+                       dw, db);
+  } else {
+    hipLaunchKernelGGL((rowln_bwd_rows_kernel<T, NG, false>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
+                       (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)nullptr, (T*)dx, dx_rs, ws, rows, W, eps);
+  }
+  return hdcm_launch_status();
+}
+
+template <typename T>
+int launch_bwd(const void* dy, int64_t dy_rs, const void* x, int64_t x_rs, const void* w, void* dx, int64_t dx_rs,
+               float* dw, float* db, float* ws, int64_t rows, int W, float eps, hipStream_t s) {
+  const int G = W / Vec<T>::N;
+  const int ng = (G + kWave - 1) / kWave;
+#define HDCM_BWD_NG(n) \
+  case n:              \
+    return launch_bwd_ng<T, n>(dy, dy_rs, x, x_rs, w, dx, dx_rs, dw, db, ws, rows, W, eps, s);
+  switch (ng) {
+    HDCM_BWD_NG(1)
+    HDCM_BWD_NG(2)
+    HDCM_BWD_NG(3)
+    HDCM_BWD_NG(4)
+    HDCM_BWD_NG(5)
+    HDCM_BWD_NG(6)
+    HDCM_BWD_NG(7)
+    HDCM_BWD_NG(8)
+    default:
+      return HDCM_EUNSUPPORTED;
+  }
+#undef HDCM_BWD_NG
+}
+
+}  // namespace
+
+extern "C" size_t hdcm_rowln_bwd_workspace_bytes(int64_t rows, int64_t width) {
+  if (rows < 0 || width <= 0) return 0;
+  return (size_t)bwd_blocks(rows) * 2 * (size_t)width * sizeof(float);
+}
+
+extern "C" int hdcm_rowln_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t x_row_stride,
+                              const void* w, void* dx, int64_t dx_row_stride, float* dw, float* db, void* ws,
+                              size_t ws_bytes, int64_t rows, int64_t width, float eps, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG((dy && x && dx) || rows == 0, HDCM_EINVAL);  // empty inputs may have no storage
+  HDCM_CHECK_ARG(!w || (dw && db), HDCM_EINVAL);
+  HDCM_CHECK_ARG(rows >= 0 && width > 0, HDCM_EINVAL);
+  const int E = 16 / hdcm_elt_size(dtype);
+  HDCM_CHECK_ARG(width % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(width / E <= 8 * kWave, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(dy_row_stride >= width && x_row_stride >= width && dx_row_stride >= width, HDCM_EINVAL);
+  HDCM_CHECK_ARG(dy_row_stride % E == 0 && x_row_stride % E == 0 && dx_row_stride % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(dy) && hdcm_aligned16(x) && hdcm_aligned16(dx), HDCM_EALIGN);
+  HDCM_CHECK_ARG(!w || hdcm_aligned16(w), HDCM_EALIGN);
+  if (w) {
+    HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_rowln_bwd_workspace_bytes(rows, width), HDCM_EWORKSPACE);
+    HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (rows == 0) {
+    if (w) {  // empty input: zero parameter gradients
+      hipLaunchKernelGGL(rowln_bwd_reduce_kernel, dim3((unsigned)((width + 255) / 256)), dim3(256), 0, s,
+                         (const float*)ws, 0, (int)width, dw, db);
+      return hdcm_launch_status();
+    }
+    return HDCM_OK;
+  }
+  if (dtype == HDCM_F32)
+    return launch_bwd<float>(dy, dy_row_stride, x, x_row_stride, w, dx, dx_row_stride, dw, db, (float*)ws, rows,
+                             (int)width, eps, s);
+  return launch_bwd<bf16_t>(dy, dy_row_stride, x, x_row_stride, w, dx, dx_row_stride, dw, db, (float*)ws, rows,
+                            (int)width, eps, s);
 }

@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 
 from . import _ops
-from .model import BlockState, HdcMamba9v3Model
+from .model import BlockState, HdcMamba9v3Model, layer_norm
 
 __all__ = ["HdcMambaLM", "DecodeGraph", "ForwardGraph", "SIZES"]
 
@@ -59,14 +59,14 @@ class HdcMambaLM(nn.Module):
         _ops._on_gpu(input_ids)
         x = self.embedding(input_ids)
         x = self.backbone(x)
-        x = _ops.layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
+        x = layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
         return self.lm_head(x)
 
     def _logits(self, x):
         """norm_f then the tied head.  The head stays on the library GEMM even for the few
         rows of a decode step: at V=50304 it streams 206 MB and hipBLASLt's skinny solution
         runs it in about 48 us against 55 us on the skinny decode kernel."""
-        x = _ops.layer_norm(x.contiguous(), self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
+        x = layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
         return self.lm_head(x)
 
     def prefill(self, input_ids, last=1):

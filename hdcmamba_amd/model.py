@@ -24,7 +24,7 @@ import torch.nn.functional as F
 from . import _ops
 
 __all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
-           "fused_norm_conv1d_trainable", "BlockState"]
+           "fused_norm_conv1d_trainable", "RowLayerNormFunction", "layer_norm", "BlockState"]
 
 
 @dataclass
@@ -75,6 +75,41 @@ def fused_norm_conv1d_trainable(x, norm_layer, conv_layer):
     return FusedNormConv1dFunction.apply(
         x, norm_layer.weight.to(x.dtype), norm_layer.bias.to(x.dtype),
         conv_layer.weight.squeeze(1).to(x.dtype), conv_layer.bias.to(x.dtype), norm_layer.eps)
+
+
+class RowLayerNormFunction(torch.autograd.Function):
+    """LayerNorm over the last dim on the HIP kernels, forward and backward, with the
+    semantics of nn.LayerNorm / F.layer_norm (fp32 statistics, output in x's dtype).
+
+    ``apply(x, weight, bias, eps)``; weight and bias may both be None (no affine).  The
+    parameter gradients are summed over rows in fp32 in a fixed order and returned in the
+    parameters' dtype.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        ctx.eps = float(eps)
+        ctx.w_dtype = weight.dtype if weight is not None else None
+        ctx.save_for_backward(x, weight)
+        return _ops.layer_norm(x.contiguous(), weight, bias, eps)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, weight = ctx.saved_tensors
+        dx, dw, db = _ops.layer_norm_bwd(grad_out.to(x.dtype), x.contiguous(), weight, ctx.eps)
+        if weight is None:
+            return dx, None, None, None
+        return dx, dw.to(ctx.w_dtype), db.to(ctx.w_dtype), None
+
+
+def layer_norm(x, weight=None, bias=None, eps=1e-5):
+    """Row LayerNorm on the HIP kernels; goes through RowLayerNormFunction when autograd
+    needs its gradient (training the residual path, norm_final and the LM's norm_f)."""
+    needs = torch.is_grad_enabled() and (x.requires_grad or any(
+        t is not None and t.requires_grad for t in (weight, bias)))
+    if needs:
+        return RowLayerNormFunction.apply(x, weight, bias, eps)
+    return _ops.layer_norm(x.contiguous(), weight, bias, eps)
 
 
 class HdcMamba9v3Block(nn.Module):
@@ -264,8 +299,7 @@ class HdcMamba9v3Model(nn.Module):
                     r[:, :pad].zero_()
                 layer._residual_step_(r)
             x = r[:, pad:]
-        return _ops.layer_norm(x.contiguous(), self.norm_final.weight, self.norm_final.bias,
-                               self.norm_final.eps)
+        return layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
 
     def prefill(self, x):
         """Forward over x [B,L,dm] (inference) that also returns every block's BlockState."""

@@ -188,6 +188,21 @@ int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out
                    const void* w, const void* b, int64_t rows, int64_t width, float eps,
                    int dtype, void* stream);
 
+/*
+ * Gradient of hdcm_rowln_fwd: dx (x's dtype) from dy and the forward input x (the row
+ * statistics are recomputed in fp32); with affine (w non-NULL) also dw = sum_rows dy*x^ and
+ * db = sum_rows dy as fp32 [width], summed in a fixed order (ws: per-workgroup partials,
+ * hdcm_rowln_bwd_workspace_bytes(rows, width) bytes; unused without affine).
+ * width/E <= 512 (E = 8 bf16, 4 fp32 elements per 16 bytes).
+ * Replaces: the autograd backward of nn.LayerNorm / F.layer_norm for norm_final
+ *           (hdcmamba/model.py:400,404), the LM's norm_f (train_fineweb.py:52,92) and the
+ *           post-LayerNorm (model.py:382).
+ */
+size_t hdcm_rowln_bwd_workspace_bytes(int64_t rows, int64_t width);
+int hdcm_rowln_bwd(const void* dy, int64_t dy_row_stride, const void* x, int64_t x_row_stride,
+                   const void* w, void* dx, int64_t dx_row_stride, float* dw, float* db, void* ws,
+                   size_t ws_bytes, int64_t rows, int64_t width, float eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

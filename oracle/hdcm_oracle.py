@@ -358,15 +358,19 @@ def faithful_slot_position(L, C):
 # --------------------------------------------------------------------------------------
 # Block / model / LM forward (model.py:331-404, train_fineweb.py:86-94)
 # --------------------------------------------------------------------------------------
-def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_states=False):
+def block_forward(p, x, cfg: BlockCfg, semantics="intended", eps=1e-5, return_states=False, mixer_grad=False):
     """One HdcMamba9v3Block forward in eval mode (model.py:386-394 + 331-384).
 
     ``p`` is the block's state_dict (tensors in the model dtype); ``x`` is [B,L,D].
     L is left-padded with zero rows to a multiple of the chunk (model.py:388-389).
+    The reference's SSM, slot and gate kernels have no autograd (model.py:340-384), so
+    its ``combined`` buffer is a constant for backward: only out_proj, the residual
+    stream and what follows the blocks receive gradients.  Autograd through this function
+    reproduces that (``combined`` is detached) unless ``mixer_grad`` is set.
     """
     C = cfg.chunk_size
     pad = (C - x.shape[1] % C) % C
-    return _block_padded(p, x, cfg, pad, 0, semantics, eps, return_states)
+    return _block_padded(p, x, cfg, pad, 0, semantics, eps, return_states, mixer_grad)
 
 
 def block_forward_stream(p, x, cfg: BlockCfg, n_prefill, eps=1e-5):
@@ -380,7 +384,7 @@ def block_forward_stream(p, x, cfg: BlockCfg, n_prefill, eps=1e-5):
     return _block_padded(p, x, cfg, pad_l, pad_r, "intended", eps, False)
 
 
-def _block_padded(p, x, cfg, pad, pad_r, semantics, eps, return_states):
+def _block_padded(p, x, cfg, pad, pad_r, semantics, eps, return_states, mixer_grad=False):
     dtype = x.dtype
     dm, ds, H, C = cfg.d_model, cfg.d_state, cfg.num_heads, cfg.chunk_size
     hd = cfg.head_dim
@@ -410,6 +414,8 @@ def _block_padded(p, x, cfg, pad, pad_r, semantics, eps, return_states):
         y_ssm_t = y_ssm
         g = gnorm_gate(y_slot, gate, p["group_norm.weight"], p["group_norm.bias"], H)
     combined = torch.cat([_rnd(y_ssm_t, dtype), _rnd(g, dtype)], -1).to(dtype)
+    if not mixer_grad:
+        combined = combined.detach()
     c = F.layer_norm(combined.float(), (ds + dm,)).to(dtype)
     res = F.linear(c, p["out_proj.weight"].to(dtype))
     out = (x + res)[:, pad:pad + L_in, :]

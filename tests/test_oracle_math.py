@@ -328,3 +328,18 @@ def test_norm_conv_bias_gradient_includes_the_halo():
     # d out[0] / d b = sum of the three halo taps + the tap on u[0] (whose b term is 1)
     want = 2 * (cw[:, 0] + cw[:, 1] + cw[:, 2] + cw[:, 3])
     torch.testing.assert_close(grads[2], want, atol=1e-5, rtol=1e-5)
+
+
+def test_oracle_training_gradients_follow_the_reference():
+    """The reference's mixer kernels have no autograd (model.py:340-384): through the oracle
+    block, out_proj and the input get gradients and the mixer's parameters none, unless
+    mixer_grad asks for the full derivative (then in_proj gets one too)."""
+    cfg = oracle.BlockCfg(64, 16, 2, 16)
+    p = oracle.init_block_params(cfg, generator_seed=3)
+    for mixer_grad in (False, True):
+        q = {k: v.detach().clone().requires_grad_(v.is_floating_point()) for k, v in p.items()}
+        x = torch.randn(1, 32, 64, generator=torch.Generator().manual_seed(4)).requires_grad_(True)
+        oracle.block_forward(q, x, cfg, mixer_grad=mixer_grad).square().sum().backward()
+        assert q["out_proj.weight"].grad is not None and x.grad is not None
+        assert (q["in_proj.weight"].grad is not None) == mixer_grad
+        assert (q["norm.weight"].grad is not None) == mixer_grad
