@@ -97,3 +97,59 @@ def test_lm_backward_matches_oracle(dev, dtype):
         for name in ("in_proj.weight", "in_proj.bias", "A_log", "decay_log", "norm.weight", "conv1d.weight",
                      "group_norm.weight"):
             assert params[f"backbone.layers.{i}.{name}"].grad is None, name
+
+
+def test_block_and_model_sum_backward(dev):
+    """``model(x).sum().backward()`` in training mode, as the reference's benchmark times the
+    backward (benchmark.py:196-205), for one block and for a two-layer model (bf16)."""
+    from hdcmamba_amd import HdcMamba9v3Block, HdcMamba9v3Model
+
+    _say("block/model sum backward")
+    cfg = oracle.BlockCfg(256, 64, 4, 64)
+    torch.manual_seed(1)
+    blk = reinit_block_(HdcMamba9v3Block(256, 64, 4, 64), seed=41, decays_uniform=True).to(torch.bfloat16).train()
+    x = torch.randn(2, 200, 256, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    sd = {k: v.detach().clone() for k, v in blk.state_dict().items()}
+    sd["gamma_buf"] = torch.exp(-F.softplus(sd["decay_log"]))
+    for v in sd.values():
+        v.requires_grad_(v.is_floating_point())
+    xr = x.clone().requires_grad_(True)
+    oracle.block_forward(sd, xr, cfg).float().sum().backward()
+    blk = blk.to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    y, none = blk(xd)
+    assert none is None
+    y.float().sum().backward()
+    assert max_rel(xd.grad, xr.grad) <= 2e-2
+    assert max_rel(blk.out_proj.weight.grad, sd["out_proj.weight"].grad) <= 2e-2
+    assert blk.in_proj.weight.grad is None
+
+    m = HdcMamba9v3Model(256, 2, 64, 32, num_heads=4, chunk_size=64).to(torch.bfloat16).to(dev).train()
+    out = m(x.to(dev))
+    out.sum().backward()
+    assert m.norm_final.weight.grad is not None
+    assert all(layer.out_proj.weight.grad is not None for layer in m.layers)
+
+
+def test_lm_step_under_autocast(dev):
+    """One optimiser step of the LM in bf16 under autocast with a cross-entropy loss, as the
+    reference's training loop runs it (train_fineweb.py:161-179): finite loss and gradient
+    norm, and the step changes exactly the parameters that have gradients."""
+    from hdcmamba_amd import HdcMambaLM
+
+    _say("lm step autocast")
+    torch.manual_seed(3)
+    lm = HdcMambaLM(256, 2, 64, 4, vocab_size=512, chunk_size=64).to(dev).to(torch.bfloat16).train()
+    opt = torch.optim.AdamW(lm.parameters(), lr=0.05)  # steps larger than a bf16 ulp of 1.0
+    ids = torch.randint(0, 512, (2, 129), device=dev)
+    before = {k: v.detach().clone() for k, v in lm.named_parameters()}
+    with torch.amp.autocast("cuda", dtype=torch.bfloat16):
+        logits = lm(ids[:, :-1])
+        loss = F.cross_entropy(logits.reshape(-1, 512).float(), ids[:, 1:].reshape(-1))
+    loss.backward()
+    norm = torch.nn.utils.clip_grad_norm_(lm.parameters(), max_norm=1.0)
+    assert torch.isfinite(loss) and torch.isfinite(norm)
+    opt.step()
+    for k, v in lm.named_parameters():
+        changed = not torch.equal(v.detach(), before[k])
+        assert changed == (v.grad is not None), k
