@@ -20,6 +20,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
 
 from . import _ops
 
@@ -261,7 +262,11 @@ class HdcMamba9v3Block(nn.Module):
         if self.training:
             with torch.no_grad():
                 self.gamma_buf.copy_(torch.exp(-F.softplus(self.decay_log)))
-        y = self._inner_forward(x.contiguous())
+            # the reference checkpoints the block body in training (model.py:391-392): only
+            # x is kept for backward and the body runs again when the gradient is needed
+            y = checkpoint(self._inner_forward, x.contiguous(), use_reentrant=False)
+        else:
+            y = self._inner_forward(x.contiguous())
         return y[:, pad:, :], None
 
 
