@@ -190,6 +190,32 @@ def test_rowln_validation():
     assert f(*a) == EUNSUPPORTED
 
 
+def test_rowln_bwd_validation():
+    lib = _ops.lib()
+    assert lib.hdcm_rowln_bwd_workspace_bytes(32768, 1024) == 1024 * 2 * 1024 * 4  # 1024 workgroups at most
+    assert lib.hdcm_rowln_bwd_workspace_bytes(10, 1024) == 3 * 2 * 1024 * 4       # ceil(10 / 4)
+    assert lib.hdcm_rowln_bwd_workspace_bytes(-1, 1024) == 0
+    # hdcm_rowln_bwd(dy, dy_rs, x, x_rs, w, dx, dx_rs, dw, db, ws, ws_bytes, rows, width, eps, dtype, stream)
+    f = lib.hdcm_rowln_bwd
+    ws_n = lib.hdcm_rowln_bwd_workspace_bytes(10, 1024)
+    base = [P16, 1024, P16, 1024, P16, P16, 1024, P16, P16, P16, ws_n, 10, 1024, 1e-5, 1, None]
+    a = list(base); a[7] = None  # affine without dw
+    assert f(*a) == EINVAL
+    a = list(base); a[10] = ws_n - 1  # short workspace
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[4] = a[7] = a[8] = a[9] = None; a[10] = 0  # no affine: no workspace needed
+    a[11] = 0
+    assert f(*a) == OK
+    a = list(base); a[12] = 1020; a[1] = a[3] = a[6] = 1020  # rows not whole 16-byte groups
+    assert f(*a) == EALIGN
+    a = list(base); a[12] = 8 * 9 * 64; a[1] = a[3] = a[6] = a[12]  # wider than the backward's tiling
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[0] = None  # null input with rows to process
+    assert f(*a) == EINVAL
+    a = list(base); a[14] = 2
+    assert f(*a) == EUNSUPPORTED
+
+
 def test_cpu_tensors_raise():
     """No CPU fallback: the product path refuses host tensors."""
     from hdcmamba_amd import HdcMamba9v3Block, HdcMamba9v3Model
