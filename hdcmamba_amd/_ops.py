@@ -129,6 +129,8 @@ def _same(t: torch.Tensor, ref: torch.Tensor, name: str) -> torch.Tensor:
 
 def _rows2d(t: torch.Tensor, name: str):
     """(row stride) of a [..., W] tensor whose rows are uniformly strided."""
+    if t.numel() == 0:  # no rows to address: any stride works, report a dense one
+        return t.shape[-1]
     if t.stride(-1) != 1:
         raise RuntimeError(f"{name}: last dimension must be contiguous")
     rs = t.stride(-2) if t.dim() >= 2 else t.shape[-1]
@@ -205,6 +207,8 @@ def norm_conv_bwd(grad_out, x, ln_w, ln_b, conv_w, eps):
     ln_b = _same(ln_b, x, "ln_b")
     conv_w = _same(conv_w.reshape(D, 4), x, "conv_w")
     grad_out = _same(grad_out, x, "grad_out")
+    if not grad_out.is_contiguous():  # e.g. the expanded gradient of a sum
+        grad_out = grad_out.contiguous()
     if x.stride(2) != 1:
         x = x.contiguous()
     dx = torch.empty(B, L, D, device=x.device, dtype=x.dtype)

@@ -290,7 +290,7 @@ extern "C" int hdcm_norm_conv_step_fwd(const void* x, int64_t x_row_stride, cons
                                        void* hist, void* out, int64_t out_row_stride, int64_t B,
                                        int64_t D, float eps, int dtype, void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(x && ln_w && ln_b && conv_w && conv_b && hist && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(ln_w && ln_b && conv_w && conv_b && ((x && hist && out) || B == 0), HDCM_EINVAL);
   HDCM_CHECK_ARG(B >= 0 && D > 0 && x_row_stride >= D && out_row_stride >= D, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(D % E == 0 && x_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
@@ -315,7 +315,8 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
                                    int64_t y_col, int64_t g_col, int64_t B, int64_t dm, int64_t ds,
                                    int64_t H, int dtype, void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(projs && A_log && h && gamma && S_prev && S_intra && gn_w && gn_b && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(A_log && gamma && gn_w && gn_b && ((projs && h && S_prev && S_intra && out) || B == 0),
+                 HDCM_EINVAL);
   HDCM_CHECK_ARG(B >= 0 && dm > 0 && ds > 0 && H > 0 && dm % H == 0 && C > 0, HDCM_EINVAL);
   HDCM_CHECK_ARG(pos >= 0 && pos < C, HDCM_EINVAL);
   HDCM_CHECK_ARG(q_col >= 3 * ds && proj_row_stride >= q_col + 4 * dm, HDCM_EINVAL);

@@ -227,13 +227,15 @@ extern "C" int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t
                                   int64_t out_row_stride, int64_t B, int64_t L, int64_t D, float eps,
                                   int dtype, void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(x && ln_w && ln_b && conv_w && conv_b && out, HDCM_EINVAL);
+  // data pointers of empty inputs (B or L zero) may be NULL
+  HDCM_CHECK_ARG(ln_w && ln_b && conv_w && conv_b && ((x && out) || B == 0 || L == 0), HDCM_EINVAL);
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && D > 0, HDCM_EINVAL);
   const int esz = hdcm_elt_size(dtype);
   const int E = 16 / esz;
   HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(D / E <= 12 * kWave, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30, HDCM_EUNSUPPORTED);
+  if (B == 0 || L == 0) return HDCM_OK;  // nothing is addressed: strides are not checked
   HDCM_CHECK_ARG(x_row_stride >= D && out_row_stride >= D, HDCM_EINVAL);
   HDCM_CHECK_ARG(x_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(x_batch_stride % E == 0 && out_batch_stride % E == 0, HDCM_EALIGN);

@@ -327,13 +327,20 @@ extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, 
                                   float* d_conv_b, void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t D,
                                   float eps, int dtype, void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(grad_out && x && ln_w && ln_b && conv_w && dx && d_ln_w && d_ln_b && d_conv_w && d_conv_b,
+  HDCM_CHECK_ARG(ln_w && ln_b && conv_w && d_ln_w && d_ln_b && d_conv_w && d_conv_b &&
+                     ((grad_out && x && dx) || B == 0 || L == 0),
                  HDCM_EINVAL);
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && D > 0, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(D / E <= 4 * kWave, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30 && (L + kChunk - 1) / kChunk <= 65535, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(hdcm_aligned16(ln_w) && hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w), HDCM_EALIGN);
+  if (B == 0 || L == 0) {  // no rows (strides unused): the parameter gradients are zero
+    hipLaunchKernelGGL(norm_conv_bwd_reduce_kernel, dim3((unsigned)((7 * D + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const float*)nullptr, 0, (int)D, d_ln_w, d_ln_b, d_conv_w, d_conv_b);
+    return hdcm_launch_status();
+  }
   HDCM_CHECK_ARG(g_row_stride >= D && x_row_stride >= D && dx_row_stride >= D, HDCM_EINVAL);
   HDCM_CHECK_ARG(g_row_stride % E == 0 && x_row_stride % E == 0 && dx_row_stride % E == 0 && g_batch_stride % E == 0 &&
                      x_batch_stride % E == 0 && dx_batch_stride % E == 0,
@@ -341,7 +348,6 @@ extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, 
   HDCM_CHECK_ARG(hdcm_aligned16(grad_out) && hdcm_aligned16(x) && hdcm_aligned16(dx) && hdcm_aligned16(ln_w) &&
                      hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w),
                  HDCM_EALIGN);
-  if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_norm_conv_bwd_workspace_bytes(B, L, D), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 255u) == 0, HDCM_EALIGN);
   hipStream_t s = (hipStream_t)stream;

@@ -201,7 +201,7 @@ extern "C" int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const v
                                     int64_t out_row_stride, int64_t M, int64_t N, int64_t K, int dtype,
                                     void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(A && W && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG((A || M == 0) && (W || N == 0) && (out || M == 0 || N == 0), HDCM_EINVAL);
   HDCM_CHECK_ARG(M >= 0 && N >= 0 && K > 0, HDCM_EINVAL);
   HDCM_CHECK_ARG(a_row_stride >= K && w_row_stride >= K && out_row_stride >= N, HDCM_EINVAL);
   HDCM_CHECK_ARG(!res || res_row_stride >= N, HDCM_EINVAL);

@@ -827,9 +827,9 @@ int launch_gate(const void* projs, int64_t prs, int64_t q_col, const void* gamma
   return hdcm_launch_status();
 }
 
-int check_projs(const void* projs, int64_t prs, int64_t q_col, int64_t dm, int dtype) {
+int check_projs(const void* projs, int64_t prs, int64_t q_col, int64_t dm, int dtype, bool empty) {
   const int E = 16 / hdcm_elt_size(dtype);
-  if (!projs) return HDCM_EINVAL;
+  if (!projs && !empty) return HDCM_EINVAL;  // empty inputs (B or L zero) may have no storage
   if (q_col < 0 || prs < q_col + 4 * dm) return HDCM_EINVAL;
   if (!hdcm_aligned16(projs) || prs % E || q_col % E || dm % E) return HDCM_EALIGN;
   return HDCM_OK;
@@ -851,7 +851,7 @@ extern "C" int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, i
   SlotPlan pl;
   int st = slot_plan(B, L, dm, H, C, dtype, &pl);
   if (st) return st;
-  st = check_projs(projs, proj_row_stride, q_col, dm, dtype);
+  st = check_projs(projs, proj_row_stride, q_col, dm, dtype, B == 0 || L == 0);
   if (st) return st;
   HDCM_CHECK_ARG(gamma != nullptr, HDCM_EINVAL);
   if (B == 0 || L == 0) return HDCM_OK;
@@ -883,9 +883,9 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
   SlotPlan pl;
   int st = slot_plan(B, L, dm, H, C, dtype, &pl);
   if (st) return st;
-  st = check_projs(projs, proj_row_stride, q_col, dm, dtype);
+  st = check_projs(projs, proj_row_stride, q_col, dm, dtype, B == 0 || L == 0);
   if (st) return st;
-  HDCM_CHECK_ARG(gamma && gn_w && gn_b && out, HDCM_EINVAL);
+  HDCM_CHECK_ARG(gamma && gn_w && gn_b && (out || B == 0 || L == 0), HDCM_EINVAL);
   const int esz = hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(out_col >= 0 && out_row_stride >= out_col + dm, HDCM_EINVAL);
   // Output runs of 4 elements must be naturally aligned (8 bytes bf16, 16 bytes fp32).

@@ -212,7 +212,7 @@ extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const vo
                             void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds, int dtype,
                             void* stream) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
-  HDCM_CHECK_ARG(projs && A_log && y, HDCM_EINVAL);
+  HDCM_CHECK_ARG(A_log && ((projs && y) || B == 0 || L == 0), HDCM_EINVAL);  // empty: NULL data allowed
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && ds > 0, HDCM_EINVAL);
   HDCM_CHECK_ARG(proj_row_stride >= 3 * ds && y_row_stride >= ds, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);

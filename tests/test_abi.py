@@ -174,8 +174,7 @@ def test_norm_conv_bwd_validation():
     assert f(*a) == EUNSUPPORTED
     a = list(base); a[20] = 250; a[2] = a[5] = a[11] = 250; a[1] = a[4] = a[10] = 64 * 250
     assert f(*a) == EALIGN
-    a = list(base); a[18] = 0
-    assert f(*a) == OK
+    # B == 0 zeroes the parameter gradients on the GPU (tests/test_gpu_block.py covers it)
 
 
 def test_rowln_validation():

@@ -159,3 +159,39 @@ def test_model_two_layers_long_context(dev):
         y = m.to(dev)(x.to(dev))
     print("max rel", max_rel(y, ref), flush=True)
     assert_close_normwise(y, ref, torch.bfloat16, "2-layer model L=32768")
+
+
+def test_empty_inputs(dev):
+    """Zero-length sequences and empty batches run through the block, the model and the LM
+    (no kernel touches the empty buffers) and give empty outputs of the right shape; the
+    LN+conv backward of an empty input gives zero parameter gradients."""
+    from hdcmamba_amd import FusedNormConv1dFunction, HdcMamba9v3Block, HdcMamba9v3Model, HdcMambaLM
+
+    print("empty inputs", flush=True)
+    torch.manual_seed(0)
+    blk = HdcMamba9v3Block(256, 64, 4, 64).to(dev).eval()
+    for shape in ((2, 0, 256), (0, 64, 256)):
+        with torch.no_grad():
+            y, _ = blk(torch.zeros(shape, device=dev))
+        assert tuple(y.shape) == shape
+    m = HdcMamba9v3Model(256, 2, 64, 32, num_heads=4, chunk_size=64).to(dev).eval()
+    with torch.no_grad():
+        assert tuple(m(torch.zeros(1, 0, 256, device=dev)).shape) == (1, 0, 256)
+    lm = HdcMambaLM(256, 1, 64, 4, vocab_size=128, chunk_size=64).to(dev).eval()
+    with torch.no_grad():
+        assert tuple(lm(torch.zeros(1, 0, dtype=torch.long, device=dev)).shape) == (1, 0, 128)
+    x = torch.zeros(2, 0, 256, device=dev, requires_grad=True)
+    w = torch.ones(256, device=dev, requires_grad=True)
+    b = torch.zeros(256, device=dev, requires_grad=True)
+    cw = torch.randn(256, 4, device=dev, requires_grad=True)
+    cb = torch.zeros(256, device=dev, requires_grad=True)
+    FusedNormConv1dFunction.apply(x, w, b, cw, cb, 1e-5).sum().backward()
+    for t in (w, b, cw, cb):
+        assert t.grad is not None and t.grad.abs().max().item() == 0.0
+    # a non-empty sum: its gradient reaches the backward as an expanded (stride-0) tensor
+    x = torch.randn(2, 5, 256, device=dev, requires_grad=True)
+    FusedNormConv1dFunction.apply(x, w, b, cw, cb, 1e-5).sum().backward()
+    xr = x.detach().cpu().requires_grad_(True)
+    ref = oracle.norm_conv(xr, w.detach().cpu(), b.detach().cpu(), cw.detach().cpu(), cb.detach().cpu(), 1e-5)
+    ref.sum().backward()
+    assert max_rel(x.grad, xr.grad) <= 1e-4
