@@ -15,6 +15,9 @@
  *    streams with distinct buffers may run concurrently.
  *  - Functions return an hdcm_status.  Arguments are validated before any
  *    HIP call, so a failed validation has no side effect.
+ *  - Empty inputs (a zero batch, sequence or row count) are valid: their data
+ *    pointers may be NULL and their strides are not checked.  Nothing is read or
+ *    written, except that gradients of parameters are set to zero.
  *
  * Reference: N01N9/hdcmamba launches Triton kernels from Python
  * (hdcmamba/model.py); each entry point below names the launch it replaces.
