@@ -176,10 +176,12 @@ __device__ __forceinline__ Frag<float> frag_scale(const Frag<float>& f, float c)
   return o;
 }
 
-// Tile loader.  The tile's q, k, v (blocks 0,1,2 relative to q_col) or only k, v
-// (B0=1, NB=2) are split into 16-byte groups; group idx = tid + 256*it covers block
-// B0 + (256*it)/(TC*GPR), row i, column group cg.  Offsets are relative to block B0.  TC*GPR is a multiple of 256, so the
-// block of each iteration is uniform and rows advance by whole tiles between calls.
+// Tile loader.  The tile's q, k, v (blocks 0,1,2) or only k, v (B0=1, NB=2) are split
+// into 16-byte groups; group idx = tid + 256*it covers block B0 + (256*it)/(TC*GPR), row i,
+// column group cg.  Block B0+k starts boff[k] columns after the tile base (the q, k, v
+// column blocks of one row buffer).  TC*GPR is a multiple of 256, so the block of each
+// iteration is uniform and rows advance by whole tiles between calls.  The row stride may
+// be negative (a sequence walked backwards from its last row).
 template <typename T, int HD, int TC, int B0, int NB>
 struct TileLoader {
   static constexpr int E = Vec<T>::N;
@@ -193,10 +195,12 @@ struct TileLoader {
   int64_t base;
   int row0;
   int64_t prs;
-  int dm;
+  int boff[NB];
   int64_t off[SCALAR ? 1 : NL];
   int row[SCALAR ? 1 : NL];
-  __device__ __forceinline__ TileLoader(int64_t prs_, int dm_, int tid) : prs(prs_), dm(dm_) {
+  __device__ __forceinline__ TileLoader(int64_t prs_, const int (&boffs)[NB], int tid) : prs(prs_) {
+#pragma unroll
+    for (int k = 0; k < NB; ++k) boff[k] = boffs[k];
     row0 = tid / GPR;
     base = (int64_t)row0 * prs + (tid % GPR) * E;
     if constexpr (!SCALAR) {
@@ -206,7 +210,7 @@ struct TileLoader {
         const int blk = B0 + (kThreads * it) / (TC * GPR);
         const int rem = idx % (TC * GPR);
         row[it] = rem / GPR;
-        off[it] = (int64_t)row[it] * prs + (blk - B0) * dm + (rem % GPR) * E;
+        off[it] = (int64_t)row[it] * prs + boff[blk - B0] + (rem % GPR) * E;
       }
     }
   }
@@ -216,7 +220,7 @@ struct TileLoader {
   }
   __device__ __forceinline__ int64_t off_of(int it) const {
     if constexpr (SCALAR)
-      return base + (int64_t)((it % IPB) * (kThreads / GPR)) * prs + (int64_t)(it / IPB) * dm;
+      return base + (int64_t)((it % IPB) * (kThreads / GPR)) * prs + boff[it / IPB];
     else return off[it];
   }
   // Always NL loads, whatever tlen (>= 1): a fixed count per tile keeps the compiler's
@@ -233,8 +237,9 @@ struct TileLoader {
 };
 
 // Write a loaded tile to LDS.  q: phi(q) row-major.  k: phi(k) row-major (unless
-// STATE_ONLY) and (phi(k)*gamma^(tlen-1-i))^T.  v: v^T.  Rows >= tlen are zero.
-template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY, bool FULL>
+// STATE_ONLY) and (phi(k)*gamma^(tlen-1-i))^T.  v: v^T.  Rows >= tlen are zero.  Without
+// PHI the feature map is the identity (q and k staged as they are).
+template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY, bool PHI, bool FULL>
 __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
                                                 int tlen, float lg2, int tid) {
   using LD = Lds<T, HD, TC>;
@@ -253,14 +258,14 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
       float f[E];
       unpack16<T>(raw[it], f);
 #pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
+      for (int e = 0; e < E; ++e) f[e] = ok ? (PHI ? phi_f(f[e]) : f[e]) : 0.f;
       store16<T>(sm + LD::oQ + i * LD::PQ + cg * E, f);
     } else if (blk == 1) {  // phi(k) row-major; k~ = round(phi(k)) * gamma^(tlen-1-i)
       float f[E], kdv[E];
       unpack16<T>(raw[it], f);
       const float kd = ok ? fexp2((float)(tlen - 1 - i) * lg2) : 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = ok ? phi_f(f[e]) : 0.f;
+      for (int e = 0; e < E; ++e) f[e] = ok ? (PHI ? phi_f(f[e]) : f[e]) : 0.f;
       if constexpr (sizeof(T) == 2) {
         // round phi(k) once, in pairs; the rounded words are stored as they are
         const bf16x8_t pk = pack_bf16x8(f);
@@ -289,18 +294,21 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
   }
 }
 
-template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY>
+template <typename T, int HD, int TC, int B0, int NB, bool STATE_ONLY, bool PHI>
 __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, TC, B0, NB>::NL], T* sm,
                                            int tlen, float lg2, int tid) {
   if (tlen == TC)
-    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, true>(raw, sm, tlen, lg2, tid);
+    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, PHI, true>(raw, sm, tlen, lg2, tid);
   else
-    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, false>(raw, sm, tlen, lg2, tid);
+    stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, PHI, false>(raw, sm, tlen, lg2, tid);
 }
 
-template <typename T, int HD, int TC, bool HAS_W, bool PAIRS>
+// PHI: feature map phi on q and k (else the identity).  EPI: GroupNorm + sigmoid gate
+// epilogue (else y itself is stored).  k, v and the gate start k_off, v_off, g_off columns
+// after q in each row.
+template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
-    const T* __restrict__ projs, int64_t prs, int q_col, int dm, int L, int C, int cshift,
+    const T* __restrict__ projs, int64_t prs, int q_col, int k_off, int v_off, int g_off, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
     int64_t ors, int out_col, float* __restrict__ S_final) {
@@ -325,9 +333,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   const int p_begin = seg * seg_tiles * TC;
   const int p_end = min(L, p_begin + seg_tiles * TC);
   const T* colbase = projs + q_col + h * HD;
-  const T* gatebase = colbase + 3 * dm;
+  const T* gatebase = colbase + g_off;
 
-  if (tid < HD) {
+  if (EPI && tid < HD) {
     sgw[tid] = to_f<T>(gn_w[h * HD + tid]);
     sgb[tid] = to_f<T>(gn_b[h * HD + tid]);
   }
@@ -349,7 +357,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     }
   }
 
-  const TL loader(prs, dm, tid);
+  const TL loader(prs, {0, k_off, v_off}, tid);
   uint4 raw[TL::NL];
   loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
 
@@ -375,12 +383,12 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
 #pragma unroll
     for (int g = 0; g < NG; ++g) graw[g] = *reinterpret_cast<const uint4*>(grow + g * gstep);
   };
-  if (w < NIT) load_gate(p_begin);
+  if (EPI && w < NIT) load_gate(p_begin);
 
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
     __syncthreads();
-    stage_tile<T, HD, TC, 0, 3, false>(raw, sm, tlen, lg2, tid);
+    stage_tile<T, HD, TC, 0, 3, false, PHI>(raw, sm, tlen, lg2, tid);
     // S_eff^T for this tile: gamma*W + gamma^(p-cs)*A (A alone when C divides TC).
     {
       float cA = 1.0f, cW = 0.0f;
@@ -478,22 +486,35 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           yacc[vt] = mma(a, pf, yacc[vt]);
         }
       }
-      // GroupNorm over the head's HD values of row iq, then the sigmoid gate.
-      float sum = 0.f;
+      // GroupNorm over the head's HD values of row iq, then the sigmoid gate (EPI); else y.
+      float mean = 0.f, rinv = 1.f;
+      if constexpr (EPI) {
+        float sum = 0.f;
 #pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
+        for (int vt = 0; vt < NVT; ++vt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sum += yacc[vt][r];
-      const float mean = quad_group_sum(sum) * (1.0f / HD);
-      float sq = 0.f;
+          for (int r = 0; r < 4; ++r) sum += yacc[vt][r];
+        mean = quad_group_sum(sum) * (1.0f / HD);
+        float sq = 0.f;
 #pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
+        for (int vt = 0; vt < NVT; ++vt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float d = yacc[vt][r] - mean;
-          sq += d * d;
+          for (int r = 0; r < 4; ++r) {
+            const float d = yacc[vt][r] - mean;
+            sq += d * d;
+          }
+        rinv = rsqrtf(quad_group_sum(sq) * (1.0f / HD) + gn_eps);
+      }
+      // output value of column vt*16 + 4*kg + r of row iq, given its gate value
+      auto out_val = [&](int vt, int r, float gv) -> float {
+        if constexpr (EPI) {
+          const int dv = vt * 16 + kg * 4 + r;
+          const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
+          return yn * frcp(1.0f + fexp(-gv));
+        } else {
+          return yacc[vt][r];
         }
-      const float rinv = rsqrtf(quad_group_sum(sq) * (1.0f / HD) + gn_eps);
+      };
       if constexpr (kPairs) {
         // Tiles vt = 2pp and 2pp+1 leave this lane 4+4 values of row iq; one
         // v_permlane16_swap per packed word trades them between the lane pairs (kg, kg^1) of
@@ -505,10 +526,13 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + gcol;
 #pragma unroll
         for (int pp = 0; pp < NG; ++pp) {
-          const uint4 gr = graw[pp];
-          const auto g0 = __builtin_amdgcn_permlane16_swap(gr.x, gr.z, false, false);
-          const auto g1 = __builtin_amdgcn_permlane16_swap(gr.y, gr.w, false, false);
-          const uint32_t gw[2][2] = {{g0[0], g1[0]}, {g0[1], g1[1]}};  // [tile of the pair][word]
+          uint32_t gw[2][2] = {{0u, 0u}, {0u, 0u}};  // [tile of the pair][word]
+          if constexpr (EPI) {
+            const uint4 gr = graw[pp];
+            const auto g0 = __builtin_amdgcn_permlane16_swap(gr.x, gr.z, false, false);
+            const auto g1 = __builtin_amdgcn_permlane16_swap(gr.y, gr.w, false, false);
+            gw[0][0] = g0[0], gw[0][1] = g1[0], gw[1][0] = g0[1], gw[1][1] = g1[1];
+          }
           uint32_t ow[2][2];
 #pragma unroll
           for (int hv = 0; hv < 2; ++hv) {
@@ -516,11 +540,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
             float o[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              const int dv = vt * 16 + kg * 4 + r;
               const uint32_t gwr = gw[hv][r >> 1];
-              const float gv = __uint_as_float((r & 1) ? (gwr & 0xffff0000u) : (gwr << 16));
-              const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
-              o[r] = yn * frcp(1.0f + fexp(-gv));
+              o[r] = out_val(vt, r, __uint_as_float((r & 1) ? (gwr & 0xffff0000u) : (gwr << 16)));
             }
             ow[hv][0] = pack_bf16x2(o[0], o[1]);
             ow[hv][1] = pack_bf16x2(o[2], o[3]);
@@ -533,19 +554,15 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + kg * 4;
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
-          float gv[4], o[4];
-          load4<T>(reinterpret_cast<const T*>(&graw[vt]), gv);
+          float gv[4] = {0.f, 0.f, 0.f, 0.f}, o[4];
+          if constexpr (EPI) load4<T>(reinterpret_cast<const T*>(&graw[vt]), gv);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int dv = vt * 16 + kg * 4 + r;
-            const float yn = (yacc[vt][r] - mean) * rinv * sgw[dv] + sgb[dv];
-            o[r] = yn * frcp(1.0f + fexp(-gv[r]));
-          }
+          for (int r = 0; r < 4; ++r) o[r] = out_val(vt, r, gv[r]);
           store4<T>(orow + vt * 16, o);
         }
       }
       // next tile's gate (this tile's again after the last: a fixed load count)
-      load_gate(p + TC < p_end ? p + TC : p);
+      if constexpr (EPI) load_gate(p + TC < p_end ? p + TC : p);
     }
 
     // ---- state update: (W or A) <- gamma^tlen * (W or A) + K~^T V
@@ -604,10 +621,11 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   }
 }
 
-// Per (segment, head, batch): U_s = sum_{j in segment} gamma^(end-1-j) k~_j^T v_j.
-template <typename T, int HD, int TC>
+// Per (segment, head, batch): U_s = sum_{j in segment} gamma^(end-1-j) k~_j^T v_j, with k~
+// from phi(k) (PHI) or k itself.  k starts at column k_col of each row, v v_off columns later.
+template <typename T, int HD, int TC, bool PHI>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(const T* __restrict__ projs,
-                                                              int64_t prs, int q_col, int dm,
+                                                              int64_t prs, int k_col, int v_off,
                                                               int L, const T* __restrict__ gamma,
                                                               int seg_tiles, int nseg,
                                                               float* __restrict__ U) {
@@ -625,7 +643,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
   const int64_t rowbase = (int64_t)b * L;
   const int p_begin = seg * seg_tiles * TC;
   const int p_end = min(L, p_begin + seg_tiles * TC);
-  const T* colbase = projs + q_col + dm + h * HD;  // k block; v follows at +dm
+  const T* colbase = projs + k_col + h * HD;
 
   f32x4_t st[OWN][NVT];
 #pragma unroll
@@ -634,13 +652,11 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
     for (int mt = 0; mt < NVT; ++mt) st[ov][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Two tiles in flight: the per-tile MFMA work is short, so one tile of prefetch would
-  // leave each step waiting for a full memory round trip.
-  // Two tiles in flight: the per-tile MFMA work is short, so one tile of prefetch would
   // leave each step waiting for a full memory round trip.  Prefetches past the segment
   // re-read the current tile, and the loop body always runs both steps (tlen = 0 makes a
   // step a no-op: zero tile, gamma^0 = 1), so every path issues the same loads in the same
   // order and the compiler's memory-counter waits stay exact.
-  const TL loader(prs, dm, tid);
+  const TL loader(prs, {0, v_off}, tid);
   uint4 raw0[TL::NL], raw1[TL::NL];
   const T* tbase = colbase + rowbase * prs;
   const int p1 = p_begin + TC < p_end ? p_begin + TC : p_begin;
@@ -649,7 +665,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
 
   auto step = [&](uint4 (&raw)[TL::NL], int p, int tlen) {
     __syncthreads();
-    stage_tile<T, HD, TC, 1, 2, true>(raw, sm, tlen, lg2, tid);
+    stage_tile<T, HD, TC, 1, 2, true, PHI>(raw, sm, tlen, lg2, tid);
     const int pn = p + 2 * TC < p_end ? p + 2 * TC : p;
     loader.load(raw, tbase + (int64_t)pn * prs, min(TC, L - pn));
     __syncthreads();
@@ -781,16 +797,17 @@ size_t slot_ws_bytes(int64_t B, int64_t H, const SlotPlan& pl) {
   return (size_t)2 * B * H * pl.nseg * pl.HD * pl.HD * sizeof(float);
 }
 
-template <typename T, int HD>
-int launch_state(const void* projs, int64_t prs, int64_t q_col, const void* gamma,
-                 const float* S0, void* ws, int64_t B, int64_t L, int64_t dm, int64_t H,
-                 const SlotPlan& pl, hipStream_t s) {
+// k at column k_col of each row, v v_off columns after k; PHI as in the kernels.
+template <typename T, int HD, bool PHI>
+int launch_state(const void* base, int64_t prs, int64_t k_col, int64_t v_off, const void* gamma,
+                 const float* S0, void* ws, int64_t B, int64_t L, int64_t H, const SlotPlan& pl,
+                 hipStream_t s) {
   constexpr int TC = TileOf<T>::value;
   float* U = (float*)ws;
   float* Ain = U + (size_t)B * H * pl.nseg * HD * HD;
   if (pl.nseg > 1) {
-    hipLaunchKernelGGL((slot_state_kernel<T, HD, TC>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
-                       dim3(kThreads), 0, s, (const T*)projs, prs, (int)q_col, (int)dm, (int)L,
+    hipLaunchKernelGGL((slot_state_kernel<T, HD, TC, PHI>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
+                       dim3(kThreads), 0, s, (const T*)base, prs, (int)k_col, (int)v_off, (int)L,
                        (const T*)gamma, pl.seg_tiles, pl.nseg, U);
     const int st = hdcm_launch_status();
     if (st) return st;
@@ -801,21 +818,23 @@ int launch_state(const void* projs, int64_t prs, int64_t q_col, const void* gamm
   return hdcm_launch_status();
 }
 
-template <typename T, int HD>
-int launch_gate(const void* projs, int64_t prs, int64_t q_col, const void* gamma,
-                const void* gn_w, const void* gn_b, float gn_eps, const void* ws, void* out,
-                int64_t ors, int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t dm,
-                int64_t H, int64_t C, const SlotPlan& pl, hipStream_t s) {
+// q at column q_col of each row; k, v and the gate k_off, v_off, g_off columns after q.
+template <typename T, int HD, bool PHI, bool EPI>
+int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int64_t v_off, int64_t g_off,
+                const void* gamma, const void* gn_w, const void* gn_b, float gn_eps, const void* ws, void* out,
+                int64_t ors, int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t H, int64_t C,
+                const SlotPlan& pl, hipStream_t s) {
   constexpr int TC = TileOf<T>::value;
   const float* Ain = (const float*)ws + (size_t)B * H * pl.nseg * HD * HD;
   // heads vary fastest so the workgroups that run together read the same rows of projs
   dim3 grid((unsigned)H, pl.nseg, (unsigned)B);
   // 16-byte output runs need 16-byte aligned rows and columns (bf16 only; fp32 always has them)
   const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0;
-#define HDCM_GATE_LAUNCH(W, P)                                                                         \
-  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P>), grid, dim3(kThreads), 0, s, (const T*)projs, prs, \
-                     (int)q_col, (int)dm, (int)L, (int)C, pl.cshift, (const T*)gamma, (const T*)gn_w,       \
-                     (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, pl.nseg, (T*)out, ors, (int)out_col, S_final)
+#define HDCM_GATE_LAUNCH(W, P)                                                                              \
+  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI>), grid, dim3(kThreads), 0, s,           \
+                     (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
+                     pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, \
+                     pl.nseg, (T*)out, ors, (int)out_col, S_final)
   if (pl.has_w) {
     if (pairs) HDCM_GATE_LAUNCH(true, true);
     else HDCM_GATE_LAUNCH(true, false);
@@ -860,7 +879,7 @@ extern "C" int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, i
   hipStream_t s = (hipStream_t)stream;
 #define HDCM_STATE_CASE(TT, HDV)                                                                  \
   if (pl.HD == HDV)                                                                              \
-    return launch_state<TT, HDV>(projs, proj_row_stride, q_col, gamma, S0, ws, B, L, dm, H, pl, s);
+    return launch_state<TT, HDV, true>(projs, proj_row_stride, q_col + dm, dm, gamma, S0, ws, B, L, H, pl, s);
   if (dtype == HDCM_BF16) {
     HDCM_STATE_CASE(bf16_t, 32)
     HDCM_STATE_CASE(bf16_t, 64)
@@ -897,8 +916,9 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
   hipStream_t s = (hipStream_t)stream;
 #define HDCM_GATE_CASE(TT, HDV)                                                                 \
   if (pl.HD == HDV)                                                                            \
-    return launch_gate<TT, HDV>(projs, proj_row_stride, q_col, gamma, gn_w, gn_b, gn_eps, ws, \
-                                out, out_row_stride, out_col, S_final, B, L, dm, H, C, pl, s);
+    return launch_gate<TT, HDV, true, true>(projs, proj_row_stride, q_col, dm, 2 * dm, 3 * dm, gamma, gn_w,  \
+                                            gn_b, gn_eps, ws, out, out_row_stride, out_col, S_final, B, L, H, \
+                                            C, pl, s);
   if (dtype == HDCM_BF16) {
     HDCM_GATE_CASE(bf16_t, 32)
     HDCM_GATE_CASE(bf16_t, 64)
@@ -909,5 +929,56 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
     HDCM_GATE_CASE(float, 96)
   }
 #undef HDCM_GATE_CASE
+  return HDCM_EUNSUPPORTED;
+}
+
+// ------------------------------------------------------------------ plain attention pass
+extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, int64_t k_col,
+                                    int64_t v_col, const void* gamma, int phi, void* ws, size_t ws_bytes,
+                                    void* out, int64_t out_row_stride, int64_t out_col, int64_t B, int64_t L,
+                                    int64_t dm, int64_t H, int64_t C, int dtype, void* stream) {
+  SlotPlan pl;
+  int st = slot_plan(B, L, dm, H, C, dtype, &pl);
+  if (st) return st;
+  HDCM_CHECK_ARG(gamma != nullptr, HDCM_EINVAL);
+  HDCM_CHECK_ARG((base && out) || B == 0 || L == 0, HDCM_EINVAL);
+  const int E = 16 / hdcm_elt_size(dtype);
+  const int64_t ars = row_stride < 0 ? -row_stride : row_stride;
+  const int64_t aors = out_row_stride < 0 ? -out_row_stride : out_row_stride;
+  HDCM_CHECK_ARG(q_col >= 0 && k_col >= 0 && v_col >= 0 && out_col >= 0, HDCM_EINVAL);
+  HDCM_CHECK_ARG(ars >= q_col + dm && ars >= k_col + dm && ars >= v_col + dm && aors >= out_col + dm, HDCM_EINVAL);
+  HDCM_CHECK_ARG(ars < ((int64_t)1 << 31) && aors < ((int64_t)1 << 31), HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(hdcm_aligned16(base) && ars % E == 0 && q_col % E == 0 && k_col % E == 0 && v_col % E == 0 &&
+                     dm % E == 0,
+                 HDCM_EALIGN);
+  HDCM_CHECK_ARG(((uintptr_t)out % 16) == 0 && out_col % 4 == 0 && aors % 4 == 0, HDCM_EALIGN);
+  if (B == 0 || L == 0) return HDCM_OK;
+  HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= slot_ws_bytes(B, H, pl), HDCM_EWORKSPACE);
+  HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
+  hipStream_t s = (hipStream_t)stream;
+#define HDCM_ATTEND_CASE(TT, HDV, PH)                                                                          \
+  if (pl.HD == HDV && (phi != 0) == PH) {                                                                    \
+    st = launch_state<TT, HDV, PH>(base, row_stride, k_col, v_col - k_col, gamma, nullptr, ws, B, L, H, pl, s); \
+    if (st) return st;                                                                                       \
+    return launch_gate<TT, HDV, PH, false>(base, row_stride, q_col, k_col - q_col, v_col - q_col, 0, gamma,   \
+                                           nullptr, nullptr, 0.f, ws, out, out_row_stride, out_col, nullptr, \
+                                           B, L, H, C, pl, s);                                              \
+  }
+  if (dtype == HDCM_BF16) {
+    HDCM_ATTEND_CASE(bf16_t, 32, true)
+    HDCM_ATTEND_CASE(bf16_t, 64, true)
+    HDCM_ATTEND_CASE(bf16_t, 96, true)
+    HDCM_ATTEND_CASE(bf16_t, 32, false)
+    HDCM_ATTEND_CASE(bf16_t, 64, false)
+    HDCM_ATTEND_CASE(bf16_t, 96, false)
+  } else {
+    HDCM_ATTEND_CASE(float, 32, true)
+    HDCM_ATTEND_CASE(float, 64, true)
+    HDCM_ATTEND_CASE(float, 96, true)
+    HDCM_ATTEND_CASE(float, 32, false)
+    HDCM_ATTEND_CASE(float, 64, false)
+    HDCM_ATTEND_CASE(float, 96, false)
+  }
+#undef HDCM_ATTEND_CASE
   return HDCM_EUNSUPPORTED;
 }

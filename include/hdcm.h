@@ -130,6 +130,25 @@ int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col
                        int64_t H, int64_t C, int dtype, void* stream);
 
 /*
+ * The slot recurrence without the GroupNorm and gate, on any three column blocks of one
+ * row buffer:  y_t = sum_{j<=t} w(t,j) (f(q_t).f(k_j)) v_j  per head, with w the slot
+ * weights above, f = phi (phi != 0) or the identity, q/k/v at columns q_col/k_col/v_col
+ * (+ h*hd) of `base`, y written to columns [out_col, out_col+dm) of `out`.  A negative
+ * row stride runs the sequence backwards: `base` (or `out`) then points at the row of the
+ * last token of the last batch and rows are reached at base + (b*L + t) * row_stride;
+ * with L a multiple of C the chunk grid maps onto itself.  Same workspace as the slot
+ * pair above (hdcm_slot_workspace_bytes).  The slot memory's backward runs it four times:
+ * to recompute y (phi, forward) and for dphi(q) (identity: q=dy, k=v, v=phi(k)), dv
+ * (backwards: q=phi(k), k=phi(q), v=dy) and dphi(k) (backwards: q=v, k=dy, v=phi(q)).
+ * No reference counterpart (the reference's slot kernel has no backward,
+ * hdcmamba/model.py:236-272,340-384); the weights are those of model.py:265-272.
+ */
+int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, int64_t k_col,
+                         int64_t v_col, const void* gamma, int phi, void* ws, size_t ws_bytes,
+                         void* out, int64_t out_row_stride, int64_t out_col, int64_t B, int64_t L,
+                         int64_t dm, int64_t H, int64_t C, int dtype, void* stream);
+
+/*
  * Recurrent decode (one token per batch row) after a prefill.  No counterpart in the
  * reference, whose only generation path re-runs the whole forward
  * (hdcmamba/train.py:139-151); the semantics are those of the chunked forward continued

@@ -50,7 +50,7 @@ import torch.nn.functional as F
 
 __all__ = [
     "BlockCfg", "kernel_rounding", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
-    "slot_sequential", "slot_chunked", "gnorm_gate", "rowln", "block_forward", "block_forward_stream",
+    "slot_sequential", "slot_chunked", "attend_sequential", "attend_chunked", "gnorm_gate", "rowln", "block_forward", "block_forward_stream",
     "model_forward", "lm_forward", "init_block_params",
 ]
 
@@ -251,7 +251,6 @@ def slot_chunked(projs, gamma, dm, ds, H, C, dtype=torch.float32, semantics="int
     q, k, v = _slot_qkv(projs, dm, ds, H)
     B, L, _, hd = q.shape
     assert L % C == 0
-    N = L // C
     qf = _rnd(phi(q), dtype)
     kf = _rnd(phi(k), dtype)
     if semantics == "faithful":
@@ -260,11 +259,37 @@ def slot_chunked(projs, gamma, dm, ds, H, C, dtype=torch.float32, semantics="int
             ones = torch.ones(B, L, H, blk - hd)
             qf = torch.cat([qf, ones], -1)
             kf = torch.cat([kf, ones], -1)
-    hk = qf.shape[-1]
+    return attend_chunked(qf, kf, v, gamma, C, dtype, S0)
+
+
+def attend_sequential(qf, kf, v, gamma, C):
+    """Brute-force y_t = sum_{j<=t} w(t,j) (qf_t.kf_j) v_j on featured q/k [B,L,H,hk] and
+    v [B,L,H,hd], with the slot weights w(t,j) = gamma^(t-j) in t's chunk and
+    gamma^(t-j-1) across chunks (model.py:265-272).  fp32, small inputs only."""
+    B, L, H, _ = qf.shape
+    g = gamma.float()
+    y = torch.zeros(B, L, H, v.shape[-1])
+    for t in range(L):
+        for j in range(t + 1):
+            e = (t - j) - (0 if t // C == j // C else 1)
+            s = (qf[:, t].float() * kf[:, j].float()).sum(-1) * g ** e  # [B,H]
+            y[:, t] += s[..., None] * v[:, j].float()
+    return y
+
+
+def attend_chunked(qf, kf, v, gamma, C, dtype=torch.float32, S0=None):
+    """The slot recurrence of slot_chunked on already featured q/k [B,L,H,hk] (phi(q),
+    phi(k), or any other tensors) and v [B,L,H,hd], chunked as model.py:254-272 orders it;
+    dot operands rounded to ``dtype`` where the reference rounds them.
+    Returns (y fp32 [B,L,H,hd], running state fp32 [B,H,hk,hd])."""
+    B, L, H, hk = qf.shape
+    hd = v.shape[-1]
+    assert L % C == 0
+    N = L // C
     # [B,H,N,C,*]
-    qf = qf.view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
-    kf = kf.view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
-    vv = v.view(B, N, C, H, hd).permute(0, 3, 1, 2, 4)
+    qf = _rnd(qf.float(), dtype).view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    kf = _rnd(kf.float(), dtype).view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    vv = v.float().view(B, N, C, H, hd).permute(0, 3, 1, 2, 4)
     lg = torch.log(gamma.float()).view(1, H, 1, 1, 1)
     idx = torch.arange(C, dtype=torch.float32)
     diff = idx[:, None] - idx[None, :]

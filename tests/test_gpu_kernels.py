@@ -159,6 +159,46 @@ def test_slot_gate_output_alignment(dev, out_col):
     assert out[..., :out_col].abs().max().item() == 0.0
 
 
+ATTEND_CASES = [
+    # (dtype, B, L, dm, H, C)
+    (torch.float32, 2, 192, 256, 4, 64),
+    (torch.bfloat16, 2, 192, 256, 4, 64),
+    (torch.bfloat16, 1, 256, 512, 8, 32),    # C < row tile
+    (torch.float32, 1, 256, 256, 4, 128),    # C > row tile: carried within-chunk state
+    (torch.bfloat16, 1, 256, 768, 8, 128),   # hd 96
+]
+
+
+@pytest.mark.parametrize("dtype,B,L,dm,H,C", ATTEND_CASES)
+@pytest.mark.parametrize("phi,reverse", [(True, False), (False, False), (False, True)])
+def test_slot_attend(dev, dtype, B, L, dm, H, C, phi, reverse):
+    """The slot recurrence without GroupNorm/gate on three column blocks of one buffer in a
+    shuffled order (v, q, k, plus an unused block), forwards or backwards in time."""
+    _say("slot_attend", dtype, B, L, dm, H, C, phi, reverse)
+    g = torch.Generator().manual_seed(L + dm + C + phi + 2 * reverse)
+    hd = dm // H
+    base = (0.5 * torch.randn(B, L, 4 * dm, generator=g)).to(dtype)
+    q_col, k_col, v_col = dm, 2 * dm, 0
+    gamma = (0.9 + 0.099 * torch.rand(H, generator=g)).to(dtype)
+    q = base[..., q_col:q_col + dm].float().view(B, L, H, hd)
+    k = base[..., k_col:k_col + dm].float().view(B, L, H, hd)
+    v = base[..., v_col:v_col + dm].float().view(B, L, H, hd)
+    if phi:
+        q, k = oracle.phi(q), oracle.phi(k)
+    if reverse:
+        q, k, v = q.flip(1), k.flip(1), v.flip(1)
+    ref, _ = oracle.attend_chunked(q, k, v, gamma, C, dtype)
+    if reverse:
+        ref = ref.flip(1)
+    out = torch.zeros(B, L, 8 + dm, device=dev, dtype=dtype)
+    _ops.slot_attend(base.to(dev), q_col, k_col, v_col, gamma.to(dev), dm, H, C, phi, out, 8, reverse=reverse)
+    assert out[..., :8].abs().max().item() == 0.0
+    got = out[..., 8:].float().cpu()
+    lim = 1e-4 if dtype == torch.float32 else 2e-2
+    err = ((got - ref.reshape(B, L, dm)).abs().max() / ref.abs().max()).item()
+    assert err <= lim, err
+
+
 def test_slot_segments_env(dev, monkeypatch):
     """Different segment lengths (state pre-pass on/off) give the same result."""
     dm, ds, H, C, B, L = 256, 64, 4, 64, 1, 1024

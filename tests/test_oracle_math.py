@@ -343,3 +343,39 @@ def test_oracle_training_gradients_follow_the_reference():
         assert q["out_proj.weight"].grad is not None and x.grad is not None
         assert (q["in_proj.weight"].grad is not None) == mixer_grad
         assert (q["norm.weight"].grad is not None) == mixer_grad
+
+
+@pytest.mark.parametrize("C", [4, 8, 32])
+def test_attend_chunked_equals_brute_force(C):
+    """The chunked slot recurrence on arbitrary (signed) featured q/k equals the brute-force
+    double loop with the gamma^(t-j) / gamma^(t-j-1) weights."""
+    g = torch.Generator().manual_seed(C)
+    B, L, H, hk, hd = 2, 32, 3, 8, 5
+    qf, kf = torch.randn(B, L, H, hk, generator=g), torch.randn(B, L, H, hk, generator=g)
+    v = torch.randn(B, L, H, hd, generator=g)
+    gamma = torch.tensor([0.9, 0.6, 1.0])
+    y, _ = oracle.attend_chunked(qf, kf, v, gamma, C)
+    ref = oracle.attend_sequential(qf, kf, v, gamma, C)
+    torch.testing.assert_close(y, ref, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("C", [4, 16])
+def test_attend_gradients_are_attend_passes(C):
+    """The three gradient contractions of the slot recurrence are the recurrence itself
+    (autograd through the brute force pins them): dq = attend(dy, v, k) forward in time,
+    dv = attend(k, q, dy) and dk = attend(v, dy, q) backward in time (L a multiple of C,
+    so the chunk grid maps onto itself)."""
+    g = torch.Generator().manual_seed(100 + C)
+    B, L, H, hk = 1, 32, 2, 6
+    qf = torch.randn(B, L, H, hk, generator=g).requires_grad_(True)
+    kf = torch.randn(B, L, H, hk, generator=g).requires_grad_(True)
+    v = torch.randn(B, L, H, hk, generator=g).requires_grad_(True)
+    dy = torch.randn(B, L, H, hk, generator=g)
+    gamma = torch.tensor([0.8, 0.95])
+    (oracle.attend_sequential(qf, kf, v, gamma, C) * dy).sum().backward()
+    fl = lambda t: t.detach().flip(1)
+    dq = oracle.attend_chunked(dy, v.detach(), kf.detach(), gamma, C)[0]
+    dv = oracle.attend_chunked(fl(kf), fl(qf), fl(dy), gamma, C)[0].flip(1)
+    dk = oracle.attend_chunked(fl(v), fl(dy), fl(qf), gamma, C)[0].flip(1)
+    for name, got, ref in (("dq", dq, qf.grad), ("dv", dv, v.grad), ("dk", dk, kf.grad)):
+        torch.testing.assert_close(got, ref, atol=1e-4, rtol=1e-4, msg=name)
