@@ -8,6 +8,7 @@ from .model import (
     HdcMamba9v3Block,
     HdcMamba9v3Model,
     fused_norm_conv1d_trainable,
+    set_differentiable_mixer,
 )
 from .lm import DecodeGraph, ForwardGraph, HdcMambaLM
 
@@ -20,4 +21,5 @@ __all__ = [
     "BlockState",
     "DecodeGraph",
     "ForwardGraph",
+    "set_differentiable_mixer",
 ]

@@ -29,6 +29,17 @@ _PROTOS = {
     "hdcm_ssm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "hdcm_ssm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                              c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_ssm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
+    "hdcm_ssm_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                             c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_gnorm_gate_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
+    "hdcm_gnorm_gate_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_float, c_void_p,
+                                    c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+                                    c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_slot_phi_prep": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
+                                   c_void_p]),
+    "hdcm_slot_phi_chain": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int,
+                                    c_void_p]),
     "hdcm_slot_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
     "hdcm_slot_state_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t,
                                     c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
@@ -246,6 +257,63 @@ def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
         B, L, d_state, _dtype(projs), _stream(projs)))
     timer.end("ssm", ev)
     return y
+
+
+def ssm_bwd(projs, A_log, d_state, h, gy, dprojs):
+    """Gradient of ssm (zero start state): d dt_raw, d x, d b into dprojs[..., :3*ds] (in
+    place) and returns d A_log (fp32 [ds]).  h is the forward's y, gy its gradient."""
+    _on_gpu(projs, h, gy, dprojs)
+    B, L, _ = projs.shape
+    A_log = _same(A_log, projs, "A_log")
+    for name, t in (("h", h), ("gy", gy), ("dprojs", dprojs)):
+        if t.dtype != projs.dtype:
+            raise RuntimeError(f"ssm_bwd: {name} must have projs' dtype")
+    dA = torch.empty(d_state, device=projs.device, dtype=torch.float32)
+    nbytes = lib().hdcm_ssm_bwd_workspace_bytes(B, L, d_state, _dtype(projs))
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=projs.device)
+    _check("hdcm_ssm_bwd", lib().hdcm_ssm_bwd(
+        projs.data_ptr(), _rows2d(projs, "projs"), A_log.data_ptr(), h.data_ptr(), _rows2d(h, "h"), gy.data_ptr(),
+        _rows2d(gy, "gy"), dprojs.data_ptr(), _rows2d(dprojs, "dprojs"), dA.data_ptr(), ws.data_ptr(), ws.numel(),
+        B, L, d_state, _dtype(projs), _stream(projs)))
+    return dA
+
+
+def gnorm_gate_bwd(y, gate, gn_w, gn_b, eps, dout, num_heads, dy, dgate):
+    """Gradient of the slot GroupNorm + gate on [B,L,dm] views: writes dy and dgate (in
+    place; column slices allowed) and returns (d gn_w, d gn_b) fp32."""
+    _on_gpu(y, gate, dout, dy, dgate)
+    B, L, dm = y.shape
+    gn_w, gn_b = _same(gn_w, y, "gn_w"), _same(gn_b, y, "gn_b")
+    f32 = dict(device=y.device, dtype=torch.float32)
+    dgw, dgb = torch.empty(dm, **f32), torch.empty(dm, **f32)
+    nbytes = lib().hdcm_gnorm_gate_bwd_workspace_bytes(dm, num_heads)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=y.device)
+    _check("hdcm_gnorm_gate_bwd", lib().hdcm_gnorm_gate_bwd(
+        y.data_ptr(), _rows2d(y, "y"), gate.data_ptr(), _rows2d(gate, "gate"), gn_w.data_ptr(), gn_b.data_ptr(),
+        float(eps), dout.data_ptr(), _rows2d(dout, "dout"), dy.data_ptr(), _rows2d(dy, "dy"), dgate.data_ptr(),
+        _rows2d(dgate, "dgate"), dgw.data_ptr(), dgb.data_ptr(), ws.data_ptr(), ws.numel(), B * L, dm, num_heads,
+        _dtype(y), _stream(y)))
+    return dgw, dgb
+
+
+def slot_phi_prep(projs, q_col, d_model, z):
+    """z[..., dm:4dm] = [v | phi(k) | phi(q)] from the q, k, v blocks of projs."""
+    _on_gpu(projs, z)
+    B, L, _ = projs.shape
+    _check("hdcm_slot_phi_prep", lib().hdcm_slot_phi_prep(
+        projs.data_ptr(), _rows2d(projs, "projs"), q_col, z.data_ptr(), _rows2d(z, "z"), B * L, d_model,
+        _dtype(projs), _stream(projs)))
+    return z
+
+
+def slot_phi_chain(projs, q_col, d_model, dprojs):
+    """In place: the q, k blocks of dprojs (gradients of phi(q), phi(k)) times phi'(q), phi'(k)."""
+    _on_gpu(projs, dprojs)
+    B, L, _ = projs.shape
+    _check("hdcm_slot_phi_chain", lib().hdcm_slot_phi_chain(
+        projs.data_ptr(), _rows2d(projs, "projs"), q_col, dprojs.data_ptr(), _rows2d(dprojs, "dprojs"), B * L,
+        d_model, _dtype(projs), _stream(projs)))
+    return dprojs
 
 
 def slot_workspace(projs, d_model, num_heads, chunk):

@@ -25,7 +25,8 @@ from torch.utils.checkpoint import checkpoint
 from . import _ops
 
 __all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
-           "fused_norm_conv1d_trainable", "RowLayerNormFunction", "layer_norm", "BlockState"]
+           "fused_norm_conv1d_trainable", "RowLayerNormFunction", "layer_norm", "SlotSsmMixerFunction",
+           "set_differentiable_mixer", "BlockState"]
 
 
 @dataclass
@@ -113,16 +114,72 @@ def layer_norm(x, weight=None, bias=None, eps=1e-5):
     return _ops.layer_norm(x.contiguous(), weight, bias, eps)
 
 
+class SlotSsmMixerFunction(torch.autograd.Function):
+    """The block's SSM and slot memory + GroupNorm/gate on the HIP kernels, differentiable.
+
+    ``apply(projs, A_log, gamma, gn_w, gn_b, d_state, d_model, num_heads, chunk)`` returns
+    the ``combined`` rows [y_ssm | gated slot output] of the forward (model.py:345-380).
+    The backward (no counterpart in the reference, whose kernels have no autograd) returns
+    the gradients of projs, A_log and the GroupNorm parameters; gamma (the slot decay, a
+    buffer refreshed from decay_log) is treated as a constant.  Slot part: y recomputed by
+    the plain recurrence, the GroupNorm/gate backward, then three passes of the recurrence
+    for d phi(q), d v and d phi(k) (the last two backwards in time) and the phi' chain;
+    SSM part: the adjoint scan from the forward's y.
+    """
+
+    @staticmethod
+    def forward(ctx, projs, A_log, gamma, gn_w, gn_b, ds, dm, H, C):
+        B, L, _ = projs.shape
+        combined = torch.empty(B, L, ds + dm, device=projs.device, dtype=projs.dtype)
+        _ops.ssm(projs, A_log, ds, combined[..., :ds])
+        ws = _ops.slot_workspace(projs, dm, H, C)
+        _ops.slot_state(projs, 3 * ds, gamma, dm, H, C, ws)
+        _ops.slot_gate(projs, 3 * ds, gamma, gn_w, gn_b, 1e-5, ws, combined, ds, dm, H, C)
+        ctx.save_for_backward(projs, A_log, gamma, gn_w, gn_b, combined)
+        ctx.dims = (ds, dm, H, C)
+        return combined
+
+    @staticmethod
+    def backward(ctx, dcomb):
+        projs, A_log, gamma, gn_w, gn_b, combined = ctx.saved_tensors
+        ds, dm, H, C = ctx.dims
+        B, L, _ = projs.shape
+        dcomb = dcomb.to(projs.dtype).contiguous()
+        q_col, g_col = 3 * ds, 3 * ds + 3 * dm
+        dprojs = torch.empty_like(projs)
+        ws = _ops.slot_workspace(projs, dm, H, C)
+        y = torch.empty(B, L, dm, device=projs.device, dtype=projs.dtype)
+        _ops.slot_attend(projs, q_col, q_col + dm, q_col + 2 * dm, gamma, dm, H, C, True, y, 0, ws=ws)
+        z = torch.empty(B, L, 4 * dm, device=projs.device, dtype=projs.dtype)  # [dy | v | phi(k) | phi(q)]
+        dgw, dgb = _ops.gnorm_gate_bwd(y, projs[..., g_col:], gn_w, gn_b, 1e-5, dcomb[..., ds:], H,
+                                       z[..., :dm], dprojs[..., g_col:])
+        _ops.slot_phi_prep(projs, q_col, dm, z)
+        _ops.slot_attend(z, 0, dm, 2 * dm, gamma, dm, H, C, False, dprojs, q_col, ws=ws)  # d phi(q)
+        _ops.slot_attend(z, 2 * dm, 3 * dm, 0, gamma, dm, H, C, False, dprojs, q_col + 2 * dm, reverse=True,
+                         ws=ws)  # d v
+        _ops.slot_attend(z, dm, 0, 3 * dm, gamma, dm, H, C, False, dprojs, q_col + dm, reverse=True,
+                         ws=ws)  # d phi(k)
+        _ops.slot_phi_chain(projs, q_col, dm, dprojs)
+        dA = _ops.ssm_bwd(projs, A_log, ds, combined[..., :ds], dcomb[..., :ds], dprojs)
+        return (dprojs, dA.to(A_log.dtype), None, dgw.to(gn_w.dtype), dgb.to(gn_b.dtype), None, None, None, None)
+
+
 class HdcMamba9v3Block(nn.Module):
     """SSM + slot-memory block (hdcmamba/model.py:300-394).
 
     ``forward(x[B,L,d_model]) -> (y[B,L,d_model], None)``.  L is left-padded with zero
     rows to a multiple of ``chunk_size`` and the pad is sliced off the output
     (model.py:388-389,394).
+
+    As in the reference, backward reaches out_proj and the residual only: the SSM and slot
+    kernels are constants for autograd.  With ``differentiable_mixer = True`` (an added
+    option) the training forward runs them through SlotSsmMixerFunction instead, so
+    in_proj, the LN+conv, A_log and the GroupNorm receive gradients too.
     """
 
-    def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256):
+    def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False):
         super().__init__()
+        self.differentiable_mixer = differentiable_mixer
         self.d_model, self.d_state = d_model, d_state
         self.num_heads, self.chunk_size = num_heads, chunk_size
         self.head_dim = d_model // num_heads
@@ -180,10 +237,27 @@ class HdcMamba9v3Block(nn.Module):
         _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
 
+    def _differentiable_mixer(self, x):
+        """_mixer with autograd through every stage (differentiable_mixer)."""
+        B, L, dm = x.shape
+        ds, H, C = self.d_state, self.num_heads, self.chunk_size
+        dtype = x.dtype
+        x_conv = fused_norm_conv1d_trainable(x, self.norm, self.conv1d)
+        projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
+        # gamma is a constant here (the buffer may carry its construction graph, as in the
+        # reference's register_buffer of exp(-softplus(decay_log)))
+        combined = SlotSsmMixerFunction.apply(projs, self.A_log.to(dtype), self.gamma_buf.detach().to(dtype),
+                                              self.group_norm.weight.to(dtype), self.group_norm.bias.to(dtype),
+                                              ds, dm, H, C)
+        return layer_norm(combined, eps=1e-5).view(B * L, ds + dm)
+
     def _inner_forward(self, x, state=None):
         """Block body on a chunk-aligned [B,L,dm] input; returns x + out_proj(LN(combined))."""
         B, L, dm = x.shape
-        c = self._mixer(x, state)
+        if self.differentiable_mixer and state is None and torch.is_grad_enabled():
+            c = self._differentiable_mixer(x)
+        else:
+            c = self._mixer(x, state)
         out = torch.addmm(x.reshape(B * L, dm), c, self.out_proj.weight.to(x.dtype).t())
         return out.view(B, L, dm)
 
@@ -335,3 +409,12 @@ class HdcMamba9v3Model(nn.Module):
             for layer, st in zip(self.layers, states):
                 x = layer.step(x, st, pos_dev)
         return _ops.layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
+
+
+def set_differentiable_mixer(module, enabled=True):
+    """Switch every HdcMamba9v3Block inside ``module`` to (or back from) the differentiable
+    mixer; returns ``module``."""
+    for m in module.modules():
+        if isinstance(m, HdcMamba9v3Block):
+            m.differentiable_mixer = bool(enabled)
+    return module

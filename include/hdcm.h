@@ -98,6 +98,21 @@ int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
                  int dtype, void* stream);
 
 /*
+ * Gradient of hdcm_ssm_fwd from a zero start state: given gy (the gradient of y) and h (the
+ * forward's y), writes d dt_raw, d x, d b into columns [0, 3*ds) of dprojs (the dtype of
+ * projs) and d A_log (fp32 [ds], summed in a fixed order).  The adjoint g_t = gy_t +
+ * a_{t+1} g_{t+1} is scanned like the forward, rows in reverse.  ws:
+ * hdcm_ssm_bwd_workspace_bytes(B, L, ds, dtype) bytes, 256-byte aligned.
+ * No reference counterpart (the reference's scan kernels have no backward,
+ * hdcmamba/model.py:175-233,340-384); the forward is that of model.py:175-233.
+ */
+size_t hdcm_ssm_bwd_workspace_bytes(int64_t B, int64_t L, int64_t ds, int dtype);
+int hdcm_ssm_bwd(const void* projs, int64_t proj_row_stride, const void* A_log, const void* h,
+                 int64_t h_row_stride, const void* gy, int64_t gy_row_stride, void* dprojs,
+                 int64_t dprojs_row_stride, float* dA_log, void* ws, size_t ws_bytes, int64_t B,
+                 int64_t L, int64_t ds, int dtype, void* stream);
+
+/*
  * Slot memory (per-head decayed linear attention, feature map elu+1) in two
  * calls sharing one workspace.  q, k, v and gate are the column blocks
  * [q_col, q_col+dm), [+dm, +2dm), [+2dm, +3dm), [+3dm, +4dm) of projs; head h
@@ -147,6 +162,34 @@ int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, in
                          int64_t v_col, const void* gamma, int phi, void* ws, size_t ws_bytes,
                          void* out, int64_t out_row_stride, int64_t out_col, int64_t B, int64_t L,
                          int64_t dm, int64_t H, int64_t C, int dtype, void* stream);
+
+/*
+ * Gradient of the per-token, per-head GroupNorm (eps, affine gn_w/gn_b over hd = dm/H
+ * values) and sigmoid gate of hdcm_slot_gate_fwd, on `rows` token rows: from y (the slot
+ * recurrence's output before the GroupNorm), the gate values and dout, writes dy and dgate
+ * (activation dtype) and d gn_w, d gn_b (fp32 [dm], summed in a fixed order).
+ * ws: hdcm_gnorm_gate_bwd_workspace_bytes(dm, H) bytes.  hd in {32, 64, 96, 128}.
+ * No reference counterpart (model.py:274-295 has no backward).
+ */
+size_t hdcm_gnorm_gate_bwd_workspace_bytes(int64_t dm, int64_t H);
+int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const void* gate, int64_t gate_row_stride,
+                        const void* gn_w, const void* gn_b, float eps, const void* dout,
+                        int64_t dout_row_stride, void* dy, int64_t dy_row_stride, void* dgate,
+                        int64_t dgate_row_stride, float* dgn_w, float* dgn_b, void* ws, size_t ws_bytes,
+                        int64_t rows, int64_t dm, int64_t H, int dtype, void* stream);
+
+/*
+ * Operands of the slot recurrence's gradient passes.  hdcm_slot_phi_prep writes, per row,
+ * v, phi(k) and phi(q) (rounded to the dtype) into column blocks [dm, 2dm), [2dm, 3dm) and
+ * [3dm, 4dm) of z (q, k, v at columns q_col, +dm, +2dm of projs).  hdcm_slot_phi_chain turns
+ * the gradients of phi(q), phi(k) held in the q and k column blocks of dprojs into those of
+ * q, k in place: multiplied by phi'(z) = 1 for z > 0, exp(z) otherwise.
+ * No reference counterpart (the feature map of model.py:261-262 has no backward).
+ */
+int hdcm_slot_phi_prep(const void* projs, int64_t proj_row_stride, int64_t q_col, void* z,
+                       int64_t z_row_stride, int64_t rows, int64_t dm, int dtype, void* stream);
+int hdcm_slot_phi_chain(const void* projs, int64_t proj_row_stride, int64_t q_col, void* dprojs,
+                        int64_t dprojs_row_stride, int64_t rows, int64_t dm, int dtype, void* stream);
 
 /*
  * Recurrent decode (one token per batch row) after a prefill.  No counterpart in the

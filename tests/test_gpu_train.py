@@ -153,3 +153,110 @@ def test_lm_step_under_autocast(dev):
     for k, v in lm.named_parameters():
         changed = not torch.equal(v.detach(), before[k])
         assert changed == (v.grad is not None), k
+
+
+# ----------------------------------------------------------------- differentiable mixer
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ssm_backward(dev, dtype):
+    """d dt_raw, d x, d b and d A_log of the scan against autograd through the oracle's
+    sequential recurrence (fp32, on the same rounded inputs); some dt_raw above the
+    softplus threshold 20."""
+    from hdcmamba_amd import _ops
+
+    _say("ssm bwd", dtype)
+    g = torch.Generator().manual_seed(5)
+    B, L, ds = 2, 300, 64
+    projs = (0.5 * torch.randn(B, L, 3 * ds + 8, generator=g)).to(dtype)
+    projs[0, 7, 3] = 25.0
+    A_log = torch.log(torch.linspace(0.5, 2.0, ds)).to(dtype)
+    gy = torch.randn(B, L, ds, generator=g).to(dtype)
+    pr = projs.float().clone().requires_grad_(True)
+    ar = A_log.float().clone().requires_grad_(True)
+    y, _ = oracle.ssm_sequential(pr, ar, ds)
+    (y * gy.float()).sum().backward()
+    pd = projs.to(dev)
+    h = torch.empty(B, L, ds, device=dev, dtype=dtype)
+    _ops.ssm(pd, A_log.to(dev), ds, h)
+    dprojs = torch.zeros(B, L, 3 * ds + 8, device=dev, dtype=dtype)
+    dA = _ops.ssm_bwd(pd, A_log.to(dev), ds, h, gy.to(dev), dprojs)
+    lim = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, got, ref in (("d dt_raw", dprojs[..., :ds], pr.grad[..., :ds]),
+                           ("d x", dprojs[..., ds:2 * ds], pr.grad[..., ds:2 * ds]),
+                           ("d b", dprojs[..., 2 * ds:3 * ds], pr.grad[..., 2 * ds:3 * ds]),
+                           ("d A_log", dA, ar.grad)):
+        err = max_rel(got, ref)
+        _say(f"  {name}: {err:.2e}")
+        assert err <= lim, (name, err)
+
+
+@pytest.mark.parametrize("dtype,H", [(torch.float32, 4), (torch.bfloat16, 4), (torch.bfloat16, 8), (torch.float32, 2)])
+def test_gnorm_gate_backward(dev, dtype, H):
+    """dy, d gate, d gn_w, d gn_b of the per-token GroupNorm + gate against autograd through
+    the oracle (head dims 64, 32 and 128)."""
+    from hdcmamba_amd import _ops
+
+    _say("gnorm gate bwd", dtype, H)
+    g = torch.Generator().manual_seed(H)
+    B, L, dm = 2, 100, 256
+    y = (2 * torch.randn(B, L, dm, generator=g) + 0.5).to(dtype)
+    gate = torch.randn(B, L, dm, generator=g).to(dtype)
+    w = (1 + 0.2 * torch.randn(dm, generator=g)).to(dtype)
+    b = (0.1 * torch.randn(dm, generator=g)).to(dtype)
+    do = torch.randn(B, L, dm, generator=g).to(dtype)
+    yr, gr, wr, br = (t.float().clone().requires_grad_(True) for t in (y, gate, w, b))
+    out = oracle.gnorm_gate(yr.view(B, L, H, dm // H), gr, wr, br, H)
+    (out * do.float()).sum().backward()
+    dy = torch.empty(B, L, dm, device=dev, dtype=dtype)
+    dg = torch.empty(B, L, dm, device=dev, dtype=dtype)
+    dgw, dgb = _ops.gnorm_gate_bwd(y.to(dev), gate.to(dev), w.to(dev), b.to(dev), 1e-5, do.to(dev), H, dy, dg)
+    lim = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, got, ref in (("dy", dy, yr.grad), ("d gate", dg, gr.grad), ("d gn_w", dgw, wr.grad),
+                           ("d gn_b", dgb, br.grad)):
+        err = max_rel(got, ref)
+        _say(f"  {name}: {err:.2e}")
+        assert err <= lim, (name, err)
+
+
+@pytest.mark.parametrize("dtype,L", [(torch.float32, 192), (torch.bfloat16, 192), (torch.float32, 100)])
+def test_differentiable_mixer_block(dev, dtype, L):
+    """A block with differentiable_mixer: gradients of every parameter but decay_log and of
+    the input against autograd through the oracle block with mixer_grad (the full derivative
+    of the intended forward, gamma held constant)."""
+    from hdcmamba_amd import HdcMamba9v3Block
+
+    _say("differentiable mixer", dtype, L)
+    cfg = oracle.BlockCfg(256, 64, 4, 64)
+    torch.manual_seed(2)
+    blk = reinit_block_(HdcMamba9v3Block(256, 64, 4, 64, differentiable_mixer=True), seed=51,
+                        decays_uniform=True).to(dtype).train()
+    with torch.no_grad():  # non-trivial LayerNorm / GroupNorm affine parameters
+        for t in (blk.norm.weight, blk.group_norm.weight):
+            t.add_(0.1 * torch.randn(t.shape, generator=torch.Generator().manual_seed(52)).to(dtype))
+        for t in (blk.norm.bias, blk.group_norm.bias):
+            t.add_(0.05 * torch.randn(t.shape, generator=torch.Generator().manual_seed(53)).to(dtype))
+    x = torch.randn(2, L, 256, generator=torch.Generator().manual_seed(54)).to(dtype)
+    R = torch.randn(2, L, 256, generator=torch.Generator().manual_seed(55))
+    sd = {k: v.detach().clone() for k, v in blk.state_dict().items()}
+    sd["gamma_buf"] = torch.exp(-F.softplus(sd["decay_log"]))
+    for v in sd.values():
+        v.requires_grad_(v.is_floating_point())
+    xr = x.clone().requires_grad_(True)
+    (oracle.block_forward(sd, xr, cfg, mixer_grad=True).float() * R).sum().backward()
+    blk = blk.to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    y, _ = blk(xd)
+    (y.float() * R.to(dev)).sum().backward()
+    lim = 1e-4 if dtype == torch.float32 else 2e-2
+    params = dict(blk.named_parameters())
+    names = ["in_proj.weight", "in_proj.bias", "A_log", "group_norm.weight", "group_norm.bias", "norm.weight",
+             "norm.bias", "conv1d.weight", "conv1d.bias", "out_proj.weight"]
+    for name in names:
+        got, ref = params[name].grad, sd[name].grad
+        assert got is not None, name
+        err = max_rel(got, ref)
+        _say(f"  {name}: {err:.2e}")
+        assert err <= lim, (name, err)
+    err = max_rel(xd.grad, xr.grad)
+    _say(f"  x: {err:.2e}")
+    assert err <= lim
+    assert params["decay_log"].grad is None
