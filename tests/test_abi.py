@@ -215,6 +215,53 @@ def test_rowln_bwd_validation():
     assert f(*a) == EUNSUPPORTED
 
 
+def test_backward_entry_points_validation():
+    lib = _ops.lib()
+    # hdcm_slot_attend_fwd(base, rs, q_col, k_col, v_col, gamma, phi, ws, ws_bytes, out, ors, out_col,
+    #                      B, L, dm, H, C, dtype, stream)
+    f = lib.hdcm_slot_attend_fwd
+    ws_n = lib.hdcm_slot_workspace_bytes(1, 128, 256, 4, 64, 1)
+    base = [P16, 1024, 256, 512, 0, P16, 0, P16, ws_n, P16, 256, 0, 1, 128, 256, 4, 64, 1, None]
+    a = list(base); a[1] = 700  # row shorter than the v block at column 512 + 256
+    assert f(*a) == EINVAL
+    a = list(base); a[3] = 516  # block not on a 16-byte boundary
+    assert f(*a) == EALIGN
+    a = list(base); a[1] = -1024; a[10] = -256; a[13] = 0  # negative strides accepted (empty: no launch)
+    assert f(*a) == OK
+    a = list(base); a[8] = ws_n - 1
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[14] = 240; a[15] = 5  # head dim 48
+    assert f(*a) == EUNSUPPORTED
+    # hdcm_ssm_bwd(projs, prs, A_log, h, hrs, gy, gyrs, dprojs, drs, dA, ws, ws_bytes, B, L, ds, dtype, stream)
+    g = lib.hdcm_ssm_bwd
+    n = lib.hdcm_ssm_bwd_workspace_bytes(1, 100, 64, 1)
+    assert n > 0 and lib.hdcm_ssm_bwd_workspace_bytes(0, 100, 64, 1) == 0
+    gb = [P16, 192, P16, P16, 64, P16, 64, P16, 192, P16, P16, n, 1, 100, 64, 1, None]
+    a = list(gb); a[9] = None  # no d A_log
+    assert g(*a) == EINVAL
+    a = list(gb); a[11] = n - 1
+    assert g(*a) == EWORKSPACE
+    a = list(gb); a[8] = 100  # dprojs rows shorter than 3*ds
+    assert g(*a) == EINVAL
+    # hdcm_gnorm_gate_bwd(y, yrs, gate, grs, gn_w, gn_b, eps, dout, dors, dy, dyrs, dgate, dgrs, dgn_w, dgn_b,
+    #                     ws, ws_bytes, rows, dm, H, dtype, stream)
+    h = lib.hdcm_gnorm_gate_bwd
+    m = lib.hdcm_gnorm_gate_bwd_workspace_bytes(256, 4)
+    assert m == 4 * 256 * 2 * 64 * 4
+    hb = [P16, 256, P16, 256, P16, P16, 1e-5, P16, 256, P16, 256, P16, 256, P16, P16, P16, m, 10, 256, 4, 1, None]
+    a = list(hb); a[19] = 5  # dm not a multiple of H
+    assert h(*a) == EINVAL
+    a = list(hb); a[18] = 240; a[19] = 5  # head dim 48
+    assert h(*a) == EUNSUPPORTED
+    a = list(hb); a[16] = m - 1
+    assert h(*a) == EWORKSPACE
+    # hdcm_slot_phi_prep / hdcm_slot_phi_chain(projs, prs, q_col, z|dprojs, rs, rows, dm, dtype, stream)
+    assert lib.hdcm_slot_phi_prep(P16, 1024, 192, P16, 800, 10, 256, 1, None) == EINVAL  # z rows < 4*dm
+    assert lib.hdcm_slot_phi_prep(P16, 1224, 196, P16, 1024, 10, 256, 1, None) == EALIGN
+    assert lib.hdcm_slot_phi_chain(P16, 600, 192, P16, 1216, 10, 256, 1, None) == EINVAL  # projs rows short
+    assert lib.hdcm_slot_phi_chain(None, 1216, 192, None, 1216, 0, 256, 1, None) == OK
+
+
 def test_cpu_tensors_raise():
     """No CPU fallback: the product path refuses host tensors."""
     from hdcmamba_amd import HdcMamba9v3Block, HdcMamba9v3Model
