@@ -122,6 +122,22 @@ __device__ __forceinline__ float wave_total(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum over aligned groups of GL lanes (GL a power of two up to 64); every lane of a group
+// receives the group's total.  Quad swaps, then the half-row and row mirrors (once the
+// smaller groups hold equal values a mirror pairs each lane with the other half), then
+// cross-row shuffles.
+template <int GL>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(GL >= 1 && GL <= 64 && (GL & (GL - 1)) == 0, "group of 2^k lanes");
+  if (GL >= 2) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+  if (GL >= 4) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+  if (GL >= 8) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+  if (GL >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
+  if (GL >= 32) v += __shfl_xor(v, 16, kWave);
+  if (GL >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
 // Sum over the four lanes l, l^16, l^32, l^48 (the row groups of an MFMA C/D tile).
 __device__ __forceinline__ float quad_group_sum(float v) {
   v += __shfl_xor(v, 16, kWave);
@@ -238,6 +254,36 @@ __device__ __forceinline__ void frag_from_f32(Frag<float>& f, const float* x) {
   for (int s = 0; s < 8; ++s) f.v[s] = x[s];
 }
 
+// ------------------------------------------------------ fixed-order column sums
+// Parameter gradients are summed over rows in two steps: each workgroup of a row pass leaves
+// one row of partial sums, then colsum_kernel adds the partial rows.  Column c of out (c <
+// ncols) is the sum over k < nk of part[base(c) + k * kstride], base(c) = (c / cgroup) *
+// gstride + c % cgroup; thread (x, j) of a 64-column x 16-row workgroup adds rows k = j,
+// j + 16, ... and the 16 sums are then added in order of j, so the result does not depend on
+// scheduling.  Columns c < nsplit go to out0[c], the others to out1[c - nsplit].
+constexpr int kSumCols = 64, kSumRows = 16;
+__global__ __launch_bounds__(kSumCols* kSumRows) static void colsum_kernel(
+    const float* __restrict__ part, int64_t kstride, int nk, int ncols, int cgroup, int64_t gstride,
+    float* __restrict__ out0, int nsplit, float* __restrict__ out1) {
+  __shared__ float acc[kSumRows][kSumCols + 1];
+  const int x = threadIdx.x % kSumCols, j = threadIdx.x / kSumCols;
+  const int c = blockIdx.x * kSumCols + x;
+  float s = 0.f;
+  if (c < ncols) {
+    const int64_t base = (int64_t)(c / cgroup) * gstride + c % cgroup;
+    for (int k = j; k < nk; k += kSumRows) s += part[base + (int64_t)k * kstride];
+  }
+  acc[j][x] = s;
+  __syncthreads();
+  if (j == 0 && c < ncols) {
+    float t = 0.f;
+#pragma unroll
+    for (int r = 0; r < kSumRows; ++r) t += acc[r][x];
+    if (c < nsplit) out0[c] = t;
+    else out1[c - nsplit] = t;
+  }
+}
+
 // Host-side dtype mapping.
 template <typename T> struct DtypeOf;
 template <> struct DtypeOf<float> { static constexpr int value = HDCM_F32; };
@@ -257,4 +303,13 @@ static inline int hdcm_elt_size(int dtype) { return dtype == HDCM_F32 ? 4 : 2; }
 static inline int hdcm_launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? HDCM_OK : HDCM_ELAUNCH;
+}
+
+// Launch colsum_kernel (see there) on `s`; nk == 0 writes zeros.
+static inline int hdcm_colsum(const float* part, int64_t kstride, int nk, int ncols, int cgroup, int64_t gstride,
+                              float* out0, int nsplit, float* out1, hipStream_t s) {
+  hipLaunchKernelGGL(hdcm::colsum_kernel, dim3((unsigned)((ncols + hdcm::kSumCols - 1) / hdcm::kSumCols)),
+                     dim3(hdcm::kSumCols * hdcm::kSumRows), 0, s, part, kstride, nk, ncols, cgroup, gstride, out0,
+                     nsplit, out1);
+  return hdcm_launch_status();
 }

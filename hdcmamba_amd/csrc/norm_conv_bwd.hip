@@ -15,9 +15,9 @@
 // norm_conv_bwd_rows_kernel: one wave per 16-row run, lanes own 16-byte column groups (as
 // the forward); a ring holds go[t..t+3]; writes dx and the row statistics (mu_t, r_t).
 // norm_conv_bwd_cols_kernel: thread = one 16-byte column group x one chunk of rows; walks
-// the chunk keeping go[t..t+3] and u[t-3..t] in registers and writes the seven column sums
-// of its chunk.  norm_conv_bwd_reduce_kernel sums the chunks in a fixed order (the result
-// does not depend on scheduling).
+// the chunk keeping go[t..t+3] and u[t-3..t] in registers, with the next four rows' loads in
+// flight while the current four are summed, and writes the seven column sums of its chunk.  colsum_kernel sums the chunks in a fixed order (the result does not depend
+// on scheduling).
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -26,7 +26,8 @@ namespace {
 
 constexpr int kRowsWPB = 4;   // waves per workgroup, rows kernel
 constexpr int kRunRows = 16;  // rows per wave, rows kernel
-constexpr int kChunk = 256;   // rows per chunk, column kernel
+constexpr int kChunk = 64;    // rows per chunk, column kernel
+constexpr int kStep = 4;      // rows loaded ahead, column kernel
 constexpr int kColThreads = 64;
 
 template <typename T, int NG>
@@ -149,7 +150,6 @@ __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
   }
 }
 
-// part layout per chunk: [7][D] = dg, db, dcb, dw0, dw1, dw2, dw3
 template <typename T>
 __global__ __launch_bounds__(kColThreads) void norm_conv_bwd_cols_kernel(
     const T* __restrict__ go, int64_t g_bs, int64_t g_rs, const T* __restrict__ x, int64_t x_bs, int64_t x_rs,
@@ -179,23 +179,17 @@ __global__ __launch_bounds__(kColThreads) void norm_conv_bwd_cols_kernel(
 #pragma unroll
       for (int k = 0; k < 4; ++k) cw[k][e] = c4[4 * e + k];
   }
-  auto xh_of = [&](int t, float (&xh)[E]) {  // (x[t] - mu_t) r_t
-    float xv[E];
-    load16<T>(xb + (int64_t)t * x_rs, xv);
-    const float2 s = st[t];
-#pragma unroll
-    for (int e = 0; e < E; ++e) xh[e] = (xv[e] - s.x) * s.y;
-  };
   auto u_of = [&](int t, float (&u)[E]) {  // u[t] = xh[t] g + b, or b before the sequence start
     if (t < 0) {
 #pragma unroll
       for (int e = 0; e < E; ++e) u[e] = gbias[e];
       return;
     }
-    float xh[E];
-    xh_of(t, xh);
+    float xv[E];
+    load16<T>(xb + (int64_t)t * x_rs, xv);
+    const float2 sv = st[t];
 #pragma unroll
-    for (int e = 0; e < E; ++e) u[e] = xh[e] * gw[e] + gbias[e];
+    for (int e = 0; e < E; ++e) u[e] = (xv[e] - sv.x) * sv.y * gw[e] + gbias[e];
   };
   auto go_of = [&](int t, float (&g)[E]) {
     if (t < L) {
@@ -203,6 +197,21 @@ __global__ __launch_bounds__(kColThreads) void norm_conv_bwd_cols_kernel(
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) g[e] = 0.f;
+    }
+  };
+  // raw 16-byte groups of kStep rows: go[t+3+i], x[t+i] and (mu, r) of row t+i
+  auto fetch = [&](int t, uint4 (&rg)[kStep], uint4 (&rx)[kStep], float (&rm)[kStep], float (&rr)[kStep]) {
+#pragma unroll
+    for (int i = 0; i < kStep; ++i) {
+      rg[i] = rx[i] = make_uint4(0, 0, 0, 0);
+      rm[i] = rr[i] = 0.f;
+      if (t + 3 + i < L) rg[i] = ldg16(gb + (int64_t)(t + 3 + i) * g_rs);
+      if (t + i < t1) {
+        rx[i] = ldg16(xb + (int64_t)(t + i) * x_rs);
+        const float2 sv = st[t + i];
+        rm[i] = sv.x;
+        rr[i] = sv.y;
+      }
     }
   };
 
@@ -219,63 +228,81 @@ __global__ __launch_bounds__(kColThreads) void norm_conv_bwd_cols_kernel(
   go_of(t0, g0);
   go_of(t0 + 1, g1);
   go_of(t0 + 2, g2);
+  uint4 ng[kStep], nx[kStep];
+  float nm[kStep], nr[kStep];
+  fetch(t0, ng, nx, nm, nr);
 #pragma unroll 1
-  for (int t = t0; t < t1; ++t) {
-    float g3[E], xh[E];
-    go_of(t + 3, g3);
-    xh_of(t, xh);
+  for (int tb = t0; tb < t1; tb += kStep) {
+    uint4 cg[kStep], cx[kStep];
+    float cm[kStep], cr[kStep];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float u0 = xh[e] * gw[e] + gbias[e];
-      const float gu = cw[3][e] * g0[e] + cw[2][e] * g1[e] + cw[1][e] * g2[e] + cw[0][e] * g3[e];
-      acc[0][e] += gu * xh[e];      // dg
-      acc[1][e] += gu;              // db (rows t >= 0)
-      acc[2][e] += g0[e];           // dcb
-      acc[3][e] += g0[e] * u3[e];   // dw0
-      acc[4][e] += g0[e] * u2[e];   // dw1
-      acc[5][e] += g0[e] * u1[e];   // dw2
-      acc[6][e] += g0[e] * u0;      // dw3
-      u3[e] = u2[e];
-      u2[e] = u1[e];
-      u1[e] = u0;
+    for (int i = 0; i < kStep; ++i) {
+      cg[i] = ng[i];
+      cx[i] = nx[i];
+      cm[i] = nm[i];
+      cr[i] = nr[i];
     }
-    // the b of the rows before the sequence start feeds out[t] for t < 3
-    if (t < 3) {
+    if (tb + kStep < t1) fetch(tb + kStep, ng, nx, nm, nr);  // next rows in flight while these are summed
 #pragma unroll
-      for (int e = 0; e < E; ++e)
+    for (int i = 0; i < kStep; ++i) {
+      const int t = tb + i;
+      if (t >= t1) continue;  // uniform: rows past the chunk
+      float g3[E], xh[E];
+      unpack16<T>(cg[i], g3);
+      unpack16<T>(cx[i], xh);
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-          if (t - 3 + k < 0) acc[1][e] += cw[k][e] * g0[e];
-    }
+      for (int e = 0; e < E; ++e) {
+        xh[e] = (xh[e] - cm[i]) * cr[i];
+        const float u0 = xh[e] * gw[e] + gbias[e];
+        const float gu = cw[3][e] * g0[e] + cw[2][e] * g1[e] + cw[1][e] * g2[e] + cw[0][e] * g3[e];
+        acc[0][e] += gu * xh[e];      // dg
+        acc[1][e] += gu;              // db (rows t >= 0)
+        acc[2][e] += g0[e];           // dcb
+        acc[3][e] += g0[e] * u3[e];   // dw0
+        acc[4][e] += g0[e] * u2[e];   // dw1
+        acc[5][e] += g0[e] * u1[e];   // dw2
+        acc[6][e] += g0[e] * u0;      // dw3
+        u3[e] = u2[e];
+        u2[e] = u1[e];
+        u1[e] = u0;
+      }
+      // the b of the rows before the sequence start feeds out[t] for t < 3
+      if (t < 3) {
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      g0[e] = g1[e];
-      g1[e] = g2[e];
-      g2[e] = g3[e];
+        for (int e = 0; e < E; ++e)
+#pragma unroll
+          for (int k = 0; k < 3; ++k)
+            if (t - 3 + k < 0) acc[1][e] += cw[k][e] * g0[e];
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        g0[e] = g1[e];
+        g1[e] = g2[e];
+        g2[e] = g3[e];
+      }
     }
   }
-  float* pp = part + ((int64_t)b * nchunk + chunk) * 7 * D + c0;
+  // part row: [dg (D) | db (D) | dcb (D) | dw (D x 4, the layout of conv_w)]
+  float* pp = part + ((int64_t)b * nchunk + chunk) * 7 * D;
 #pragma unroll
-  for (int j = 0; j < 7; ++j)
+  for (int j = 0; j < 3; ++j)
 #pragma unroll
-    for (int e = 0; e < E; ++e) pp[(int64_t)j * D + e] = acc[j][e];
+    for (int e = 0; e < E; ++e) pp[(int64_t)j * D + c0 + e] = acc[j][e];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) pp[3 * (int64_t)D + (int64_t)(c0 + e) * 4 + k] = acc[3 + k][e];
 }
 
-// out[j][c] = sum over (batch, chunk) of part[..][j][c]; j: dg, db, dcb, dw0..dw3.
-__global__ __launch_bounds__(256) void norm_conv_bwd_reduce_kernel(const float* __restrict__ part, int nparts,
-                                                                   int D, float* __restrict__ d_ln_w,
-                                                                   float* __restrict__ d_ln_b,
-                                                                   float* __restrict__ d_conv_w,
-                                                                   float* __restrict__ d_conv_b) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= 7 * D) return;
-  const int j = idx / D, c = idx % D;
-  float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += part[(int64_t)p * 7 * D + idx];
-  if (j == 0) d_ln_w[c] = s;
-  else if (j == 1) d_ln_b[c] = s;
-  else if (j == 2) d_conv_b[c] = s;
-  else d_conv_w[(int64_t)c * 4 + (j - 3)] = s;
+// Sum the part rows (nparts of them) into the four parameter gradients.
+int reduce_parts(const float* part, int nparts, int64_t D, float* d_ln_w, float* d_ln_b, float* d_conv_w,
+                 float* d_conv_b, hipStream_t s) {
+  const int64_t ks = 7 * D;
+  int st = hdcm_colsum(part, ks, nparts, 2 * (int)D, 2 * (int)D, 0, d_ln_w, (int)D, d_ln_b, s);
+  if (!st) st = hdcm_colsum(part ? part + 2 * D : part, ks, nparts, (int)D, (int)D, 0, d_conv_b, (int)D, nullptr, s);
+  if (!st) st = hdcm_colsum(part ? part + 3 * D : part, ks, nparts, 4 * (int)D, 4 * (int)D, 0, d_conv_w, 4 * (int)D,
+                            nullptr, s);
+  return st;
 }
 
 int64_t chunks_of(int64_t L) { return (L + kChunk - 1) / kChunk; }
@@ -308,9 +335,7 @@ int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_
                      (const float2*)stats, part, (int)L, (int)D, (int)nchunk);
   st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL(norm_conv_bwd_reduce_kernel, dim3((unsigned)((7 * D + 255) / 256)), dim3(256), 0, s,
-                     (const float*)part, (int)(B * nchunk), (int)D, d_ln_w, d_ln_b, d_conv_w, d_conv_b);
-  return hdcm_launch_status();
+  return reduce_parts(part, (int)(B * nchunk), D, d_ln_w, d_ln_b, d_conv_w, d_conv_b, s);
 }
 
 }  // namespace
@@ -336,11 +361,8 @@ extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, 
   HDCM_CHECK_ARG(D / E <= 4 * kWave, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30 && (L + kChunk - 1) / kChunk <= 65535, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(hdcm_aligned16(ln_w) && hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w), HDCM_EALIGN);
-  if (B == 0 || L == 0) {  // no rows (strides unused): the parameter gradients are zero
-    hipLaunchKernelGGL(norm_conv_bwd_reduce_kernel, dim3((unsigned)((7 * D + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, (const float*)nullptr, 0, (int)D, d_ln_w, d_ln_b, d_conv_w, d_conv_b);
-    return hdcm_launch_status();
-  }
+  if (B == 0 || L == 0)  // no rows (strides unused): the parameter gradients are zero
+    return reduce_parts(nullptr, 0, D, d_ln_w, d_ln_b, d_conv_w, d_conv_b, (hipStream_t)stream);
   HDCM_CHECK_ARG(g_row_stride >= D && x_row_stride >= D && dx_row_stride >= D, HDCM_EINVAL);
   HDCM_CHECK_ARG(g_row_stride % E == 0 && x_row_stride % E == 0 && dx_row_stride % E == 0 && g_batch_stride % E == 0 &&
                      x_batch_stride % E == 0 && dx_batch_stride % E == 0,

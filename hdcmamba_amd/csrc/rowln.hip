@@ -289,19 +289,6 @@ __global__ __launch_bounds__(kBwdWaves* kWave) void rowln_bwd_rows_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void rowln_bwd_reduce_kernel(const float* __restrict__ part, int nblk, int W,
-                                                               float* __restrict__ dw, float* __restrict__ db) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= W) return;
-  float a = 0.f, b = 0.f;
-  for (int k = 0; k < nblk; ++k) {
-    a += part[(int64_t)k * 2 * W + c];
-    b += part[(int64_t)k * 2 * W + W + c];
-  }
-  dw[c] = a;
-  db[c] = b;
-}
-
 template <typename T, int NG>
 int launch_bwd_ng(const void* dy, int64_t dy_rs, const void* x, int64_t x_rs, const void* w, void* dx,
                   int64_t dx_rs, float* dw, float* db, float* ws, int64_t rows, int W, float eps, hipStream_t s) {
@@ -311,8 +298,7 @@ int launch_bwd_ng(const void* dy, int64_t dy_rs, const void* x, int64_t x_rs, co
                        (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)w, (T*)dx, dx_rs, ws, rows, W, eps);
     int st = hdcm_launch_status();
     if (st) return st;
-    hipLaunchKernelGGL(rowln_bwd_reduce_kernel, dim3((unsigned)((W + 255) / 256)), dim3(256), 0, s, ws, (int)nb, W,
-                       dw, db);
+    return hdcm_colsum(ws, 2 * (int64_t)W, (int)nb, 2 * W, 2 * W, 0, dw, W, db, s);
   } else {
     hipLaunchKernelGGL((rowln_bwd_rows_kernel<T, NG, false>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
                        (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)nullptr, (T*)dx, dx_rs, ws, rows, W, eps);
@@ -370,11 +356,8 @@ extern "C" int hdcm_rowln_bwd(const void* dy, int64_t dy_row_stride, const void*
   }
   hipStream_t s = (hipStream_t)stream;
   if (rows == 0) {
-    if (w) {  // empty input: zero parameter gradients
-      hipLaunchKernelGGL(rowln_bwd_reduce_kernel, dim3((unsigned)((width + 255) / 256)), dim3(256), 0, s,
-                         (const float*)ws, 0, (int)width, dw, db);
-      return hdcm_launch_status();
-    }
+    if (w)  // empty input: zero parameter gradients
+      return hdcm_colsum((const float*)ws, 2 * width, 0, 2 * (int)width, 2 * (int)width, 0, dw, (int)width, db, s);
     return HDCM_OK;
   }
   if (dtype == HDCM_F32)

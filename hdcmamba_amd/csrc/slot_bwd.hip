@@ -15,8 +15,10 @@
 // gnorm_gate_bwd_kernel: one wave per (token, head) at a time, lane i holding column i (and
 // i + 64 when hd > 64); the waves of the grid stride over (token, head) pairs with a stride
 // that is a multiple of H, so a wave always meets the same head and keeps that head's d w,
-// d b column sums in registers; gnorm_gate_bwd_reduce_kernel adds the waves' sums in a fixed
-// order.  The feature-map kernels are elementwise over 16-byte groups.
+// d b column sums in registers; colsum_kernel adds the waves' sums in a fixed order.  Used
+// for head widths whose 16-byte groups do not form a power-of-two lane group (hd = 96);
+// gnorm_gate_bwd_rows_kernel below covers the others.  The feature-map kernels are
+// elementwise over 16-byte groups.
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -112,20 +114,110 @@ __global__ __launch_bounds__(kThreads) void gnorm_gate_bwd_kernel(
   }
 }
 
-// d w, d b of column c = h*HD + i: the waves w with w % H == h, in increasing order.
-__global__ __launch_bounds__(kThreads) void gnorm_gate_bwd_reduce_kernel(const float* __restrict__ part, int HD,
-                                                                         int H, int nwaves, float* __restrict__ dgn_w,
-                                                                         float* __restrict__ dgn_b) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= H * HD) return;
-  const int h = c / HD, i = c % HD;
-  float a = 0.f, b = 0.f;
-  for (int w = h; w < nwaves; w += H) {
-    a += part[(int64_t)w * 2 * HD + i];
-    b += part[(int64_t)w * 2 * HD + HD + i];
+// Row-stripe form of the same backward, for heads of GL = HD / E lanes with GL a power of
+// two (E values of a 16-byte group per lane).  A workgroup's four waves share one stripe of
+// 64 groups of the row (stripe = blockIdx % nstripe) and stride over tokens, so each lane
+// keeps its E columns' d w, d b sums in registers; the head statistics are GL-lane group
+// sums.  Loads and stores are 16 bytes per lane.  The four waves' sums are added in LDS in
+// wave order and each workgroup leaves part[m][2][dm] (m = blockIdx / nstripe) for
+// colsum_kernel.  The next token's three groups are loaded before the current one is used.
+template <typename T, int HD>
+__global__ __launch_bounds__(kThreads) void gnorm_gate_bwd_rows_kernel(
+    const T* __restrict__ y, int64_t y_rs, const T* __restrict__ gate, int64_t g_rs, const T* __restrict__ gn_w,
+    const T* __restrict__ gn_b, float eps, const T* __restrict__ dout, int64_t do_rs, T* __restrict__ dy,
+    int64_t dy_rs, T* __restrict__ dgate, int64_t dg_rs, float* __restrict__ part, int64_t rows, int dm,
+    int nstripe) {
+  constexpr int E = Vec<T>::N;
+  constexpr int GL = HD / E;
+  constexpr float kInvHD = 1.0f / HD;
+  __shared__ float red[kWaves][2][kWave * E];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int stripe = (int)(blockIdx.x % (unsigned)nstripe);
+  const int64_t m = blockIdx.x / (unsigned)nstripe;
+  const int64_t nblk = gridDim.x / (unsigned)nstripe;
+  const int G = dm / E;
+  const int cg = stripe * kWave + lane;
+  const bool ok = cg < G;
+  const int64_t c0 = (int64_t)cg * E;
+  float w[E], bb[E], aw[E], ab[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) aw[e] = ab[e] = w[e] = bb[e] = 0.f;
+  if (ok) {
+    load16<T>(gn_w + c0, w);
+    load16<T>(gn_b + c0, bb);
   }
-  dgn_w[c] = a;
-  dgn_b[c] = b;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  const int64_t tstep = nblk * kWaves;
+  int64_t t = m * kWaves + wv;
+  uint4 ry = zero, rg = zero, rd = zero;
+  if (ok && t < rows) {
+    ry = ldg16(y + t * y_rs + c0);
+    rg = ldg16(gate + t * g_rs + c0);
+    rd = ldg16(dout + t * do_rs + c0);
+  }
+  for (; t < rows; t += tstep) {
+    float yv[E], gv[E], dv[E];
+    unpack16<T>(ry, yv);
+    unpack16<T>(rg, gv);
+    unpack16<T>(rd, dv);
+    const int64_t tn = t + tstep;
+    if (ok && tn < rows) {
+      ry = ldg16(y + tn * y_rs + c0);
+      rg = ldg16(gate + tn * g_rs + c0);
+      rd = ldg16(dout + tn * do_rs + c0);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += yv[e];
+    const float mean = group_sum<GL>(s) * kInvHD;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      yv[e] -= mean;
+      q += yv[e] * yv[e];
+    }
+    const float rstd = rsqrtf(group_sum<GL>(q) * kInvHD + eps);
+    float dxh[E], sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float xh = yv[e] * rstd;
+      const float sg = frcp(1.0f + fexp(-gv[e]));
+      const float yn = xh * w[e] + bb[e];
+      const float dyn = dv[e] * sg;
+      gv[e] = dv[e] * yn * sg * (1.0f - sg);  // d gate
+      aw[e] += dyn * xh;
+      ab[e] += dyn;
+      dxh[e] = dyn * w[e];
+      sa += dxh[e];
+      sb += dxh[e] * xh;
+      yv[e] = xh;
+    }
+    const float ma = group_sum<GL>(sa) * kInvHD, mb = group_sum<GL>(sb) * kInvHD;
+    if (ok) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) dxh[e] = rstd * (dxh[e] - ma - yv[e] * mb);
+      store16<T>(dy + t * dy_rs + c0, dxh);
+      store16<T>(dgate + t * dg_rs + c0, gv);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    red[wv][0][lane * E + e] = aw[e];
+    red[wv][1][lane * E + e] = ab[e];
+  }
+  __syncthreads();
+  float* pm = part + m * 2 * (int64_t)dm + (int64_t)stripe * kWave * E;
+  const int width = min(kWave, G - stripe * kWave) * E;  // valid columns of this stripe
+  for (int i = threadIdx.x; i < 2 * kWave * E; i += kThreads) {
+    const int j = i / (kWave * E), c = i % (kWave * E);
+    if (c < width) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < kWaves; ++k) acc += red[k][j][c];
+      pm[(int64_t)j * dm + c] = acc;
+    }
+  }
 }
 
 // Z[row] = [-- | v | round(phi(k)) | round(phi(q))] (the first block, dy, is written by the
@@ -181,11 +273,21 @@ unsigned grid_for(int64_t n) {
   return (unsigned)(b < 4096 ? (b > 0 ? b : 1) : 4096);
 }
 
+constexpr int kStripeBlocks = 512;  // workgroups per row stripe, row-stripe kernel
+
+// Row-stripe kernel for this head width and element size?
+bool stripe_form(int64_t hd, int esz) {
+  const int64_t gl = hd * esz / 16;
+  return hd * esz % 16 == 0 && gl >= 1 && gl <= kWave && (gl & (gl - 1)) == 0;
+}
+
 }  // namespace
 
 extern "C" size_t hdcm_gnorm_gate_bwd_workspace_bytes(int64_t dm, int64_t H) {
   if (dm <= 0 || H <= 0 || dm % H) return 0;
-  return (size_t)H * kWavesPerHead * 2 * (size_t)(dm / H) * sizeof(float);
+  const size_t per_head = (size_t)H * kWavesPerHead * 2 * (size_t)(dm / H) * sizeof(float);
+  const size_t stripes = (size_t)kStripeBlocks * 2 * (size_t)dm * sizeof(float);
+  return per_head > stripes ? per_head : stripes;
 }
 
 extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const void* gate, int64_t gate_row_stride,
@@ -202,6 +304,40 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_gnorm_gate_bwd_workspace_bytes(dm, H), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
   hipStream_t s = (hipStream_t)stream;
+  if (stripe_form(hd, hdcm_elt_size(dtype))) {
+    const int E = 16 / hdcm_elt_size(dtype);
+    const int nstripe = (int)((dm / E + kWave - 1) / kWave);
+    const int64_t nblk = std::min<int64_t>(kStripeBlocks, (rows + kWaves - 1) / kWaves);
+    if (rows > 0) {
+      HDCM_CHECK_ARG(y_row_stride >= dm && gate_row_stride >= dm && dout_row_stride >= dm && dy_row_stride >= dm &&
+                         dgate_row_stride >= dm,
+                     HDCM_EINVAL);
+      HDCM_CHECK_ARG(y_row_stride % E == 0 && gate_row_stride % E == 0 && dout_row_stride % E == 0 &&
+                         dy_row_stride % E == 0 && dgate_row_stride % E == 0 && hdcm_aligned16(y) &&
+                         hdcm_aligned16(gate) && hdcm_aligned16(dout) && hdcm_aligned16(dy) && hdcm_aligned16(dgate) &&
+                         hdcm_aligned16(gn_w) && hdcm_aligned16(gn_b),
+                     HDCM_EALIGN);
+      const dim3 grid((unsigned)(nblk * nstripe));
+#define HDCM_GNS_CASE(TT, HDV)                                                                                      \
+  if (hd == HDV) {                                                                                                  \
+    hipLaunchKernelGGL((gnorm_gate_bwd_rows_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)y,            \
+                       y_row_stride, (const TT*)gate, gate_row_stride, (const TT*)gn_w, (const TT*)gn_b, eps,       \
+                       (const TT*)dout, dout_row_stride, (TT*)dy, dy_row_stride, (TT*)dgate, dgate_row_stride,      \
+                       (float*)ws, rows, (int)dm, nstripe);                                                         \
+  }
+      if (dtype == HDCM_F32) {
+        HDCM_GNS_CASE(float, 32) HDCM_GNS_CASE(float, 64) HDCM_GNS_CASE(float, 128)
+      } else {
+        HDCM_GNS_CASE(bf16_t, 32) HDCM_GNS_CASE(bf16_t, 64) HDCM_GNS_CASE(bf16_t, 128)
+      }
+#undef HDCM_GNS_CASE
+      const int st = hdcm_launch_status();
+      if (st) return st;
+    }
+    // workgroup m left part[m][2][dm]: d gn_w is the sum of part[m][0], d gn_b of part[m][1]
+    return hdcm_colsum((const float*)ws, 2 * dm, rows > 0 ? (int)nblk : 0, 2 * (int)dm, 2 * (int)dm, 0, dgn_w,
+                       (int)dm, dgn_b, s);
+  }
   const int nwaves = (int)(H * kWavesPerHead);
   if (rows > 0) {
     HDCM_CHECK_ARG(y_row_stride >= dm && gate_row_stride >= dm && dout_row_stride >= dm && dy_row_stride >= dm &&
@@ -224,10 +360,13 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
     const int st = hdcm_launch_status();
     if (st) return st;
   }
-  // with no rows the reduction sums nothing: zero gradients
-  hipLaunchKernelGGL(gnorm_gate_bwd_reduce_kernel, dim3((unsigned)((dm + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                     s, (const float*)ws, (int)hd, (int)H, rows > 0 ? nwaves : 0, dgn_w, dgn_b);
-  return hdcm_launch_status();
+  // wave w = h + H m left part[w][2][hd]: column h*hd + i of d gn_w sums part[w][0][i] over m
+  // (with no rows the sums are empty: zero gradients)
+  const int nk = rows > 0 ? nwaves / (int)H : 0;
+  const int64_t kstride = H * 2 * hd;
+  const int st = hdcm_colsum((const float*)ws, kstride, nk, (int)dm, (int)hd, 2 * hd, dgn_w, (int)dm, nullptr, s);
+  if (st) return st;
+  return hdcm_colsum((const float*)ws + hd, kstride, nk, (int)dm, (int)hd, 2 * hd, dgn_b, (int)dm, nullptr, s);
 }
 
 extern "C" int hdcm_slot_phi_prep(const void* projs, int64_t proj_row_stride, int64_t q_col, void* z,

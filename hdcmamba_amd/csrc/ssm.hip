@@ -261,7 +261,7 @@ extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const vo
 //   d A_log = sum_t g_t h_{t-1} a_t dt_t A               (A = -exp(A_log))
 // ssm_grad_kernel computes the row terms (a fixed grid of workgroups striding over rows, one
 // thread per 16-byte column group) and each workgroup's sums for d A_log, which
-// ssm_grad_reduce_kernel adds in a fixed order.
+// colsum_kernel adds in a fixed order.
 namespace {
 
 constexpr int kGradMaxBlocks = 1024;
@@ -331,15 +331,6 @@ __global__ __launch_bounds__(kThreads) void ssm_grad_kernel(
   }
 }
 
-__global__ __launch_bounds__(kThreads) void ssm_grad_reduce_kernel(const float* __restrict__ part, int nblk, int ds,
-                                                                   float* __restrict__ dA_log) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= ds) return;
-  float s = 0.f;
-  for (int k = 0; k < nblk; ++k) s += part[(int64_t)k * ds + c];
-  dA_log[c] = s;
-}
-
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 template <typename T>
@@ -376,9 +367,7 @@ int launch_bwd(const void* projs, int64_t prs, const void* A_log, const void* h,
                      hrs, (const T*)g, ds, (T*)dprojs, dprs, part, B * L, (int)L, (int)ds);
   st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL(ssm_grad_reduce_kernel, dim3((unsigned)((ds + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
-                     (const float*)part, (int)nb, (int)ds, dA_log);
-  return hdcm_launch_status();
+  return hdcm_colsum(part, ds, (int)nb, (int)ds, (int)ds, 0, dA_log, (int)ds, nullptr, s);
 }
 
 }  // namespace
@@ -402,11 +391,8 @@ extern "C" int hdcm_ssm_bwd(const void* projs, int64_t proj_row_stride, const vo
   HDCM_CHECK_ARG(B <= 65535 && ssm_tiles(L) < ((int64_t)1 << 31) && ds <= 65535 && ds / E <= kThreads,
                  HDCM_EUNSUPPORTED);
   hipStream_t s = (hipStream_t)stream;
-  if (B == 0 || L == 0) {  // no rows: d A_log is zero
-    hipLaunchKernelGGL(ssm_grad_reduce_kernel, dim3((unsigned)((ds + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       s, (const float*)nullptr, 0, (int)ds, dA_log);
-    return hdcm_launch_status();
-  }
+  if (B == 0 || L == 0)  // no rows: d A_log is zero
+    return hdcm_colsum(nullptr, ds, 0, (int)ds, (int)ds, 0, dA_log, (int)ds, nullptr, s);
   HDCM_CHECK_ARG(proj_row_stride >= 3 * ds && h_row_stride >= ds && gy_row_stride >= ds &&
                      dprojs_row_stride >= 3 * ds,
                  HDCM_EINVAL);

@@ -158,7 +158,7 @@ def test_skinny_gemm_validation():
 
 def test_norm_conv_bwd_validation():
     lib = _ops.lib()
-    assert lib.hdcm_norm_conv_bwd_workspace_bytes(1, 32768, 1024) == 32768 * 8 + 128 * 7 * 1024 * 4
+    assert lib.hdcm_norm_conv_bwd_workspace_bytes(1, 32768, 1024) == 32768 * 8 + 512 * 7 * 1024 * 4  # 64-row chunks
     assert lib.hdcm_norm_conv_bwd_workspace_bytes(0, 10, 64) == 0
     # hdcm_norm_conv_bwd(go, g_bs, g_rs, x, x_bs, x_rs, ln_w, ln_b, conv_w, dx, d_bs, d_rs,
     #                    d_ln_w, d_ln_b, d_conv_w, d_conv_b, ws, ws_bytes, B, L, D, eps, dtype, stream)
@@ -247,7 +247,7 @@ def test_backward_entry_points_validation():
     #                     ws, ws_bytes, rows, dm, H, dtype, stream)
     h = lib.hdcm_gnorm_gate_bwd
     m = lib.hdcm_gnorm_gate_bwd_workspace_bytes(256, 4)
-    assert m == 4 * 256 * 2 * 64 * 4
+    assert m == max(4 * 256 * 2 * 64 * 4, 512 * 2 * 256 * 4)  # per-head form, row-stripe form
     hb = [P16, 256, P16, 256, P16, P16, 1e-5, P16, 256, P16, 256, P16, 256, P16, P16, P16, m, 10, 256, 4, 1, None]
     a = list(hb); a[19] = 5  # dm not a multiple of H
     assert h(*a) == EINVAL

@@ -268,7 +268,8 @@ def test_skinny_gemm_in_place_residual(dev):
 
 # ----------------------------------------------------------------------------- norm_conv backward
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("B,L,D", [(2, 1, 256), (2, 5, 256), (1, 300, 1024), (2, 700, 768), (1, 64, 2048)])
+@pytest.mark.parametrize("B,L,D", [(2, 1, 256), (2, 5, 256), (1, 300, 1024), (2, 700, 768), (1, 64, 2048),
+                                   (3, 131, 512)])
 def test_norm_conv_backward(dev, dtype, B, L, D):
     """FusedNormConv1dFunction's backward against autograd through the oracle (fp64 for fp32
     inputs): dx elementwise, the parameter gradients (sums over B*L rows) normwise."""

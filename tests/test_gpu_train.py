@@ -189,15 +189,18 @@ def test_ssm_backward(dev, dtype):
         assert err <= lim, (name, err)
 
 
-@pytest.mark.parametrize("dtype,H", [(torch.float32, 4), (torch.bfloat16, 4), (torch.bfloat16, 8), (torch.float32, 2)])
-def test_gnorm_gate_backward(dev, dtype, H):
+@pytest.mark.parametrize("dtype,H,dm,B,L", [(torch.float32, 4, 256, 2, 100), (torch.bfloat16, 4, 256, 2, 100),
+                                            (torch.bfloat16, 8, 256, 2, 100), (torch.float32, 2, 256, 2, 100),
+                                            (torch.bfloat16, 8, 768, 2, 100), (torch.float32, 8, 768, 1, 70),
+                                            (torch.bfloat16, 4, 512, 1, 2600), (torch.float32, 16, 1024, 1, 2051)])
+def test_gnorm_gate_backward(dev, dtype, H, dm, B, L):
     """dy, d gate, d gn_w, d gn_b of the per-token GroupNorm + gate against autograd through
-    the oracle (head dims 64, 32 and 128)."""
+    the oracle: head dims 64, 32 and 128 (row-stripe kernel; one partial stripe at dm 256,
+    more tokens than the 2048 waves at L 2600 and 2051) and 96 (per-head kernel)."""
     from hdcmamba_amd import _ops
 
-    _say("gnorm gate bwd", dtype, H)
-    g = torch.Generator().manual_seed(H)
-    B, L, dm = 2, 100, 256
+    _say("gnorm gate bwd", dtype, H, dm, B, L)
+    g = torch.Generator().manual_seed(H + L)
     y = (2 * torch.randn(B, L, dm, generator=g) + 0.5).to(dtype)
     gate = torch.randn(B, L, dm, generator=g).to(dtype)
     w = (1 + 0.2 * torch.randn(dm, generator=g)).to(dtype)
