@@ -39,20 +39,22 @@ def _cpu_model():
     return platform.processor() or "unknown"
 
 
-def forward_totals(cfg):
+def forward_totals(cfg, fused_out_proj=True):
     """Algorithmic FLOPs and compulsory HBM bytes of one LM forward (bf16, eb=2).
 
     Per block, bytes: norm_conv (read x, write x_conv), in_proj (read x_conv and W, write
     projs), SSM (read dt/x/b, write y), slot state pre-pass (read k, v), slot_gate (read
-    q/k/v/gate, write output), rowln (read and write combined), out_proj (read combined, W
-    and the residual, write the residual).  FLOPs: in_proj, out_proj and the slot
-    contractions (dense C x C count).  Plus embedding, the two final LayerNorms and the tied
-    head (read x and the embedding, write the logits)."""
+    q/k/v/gate, write output), rowln (read and write combined; absent when the LayerNorm is
+    folded into out_proj), out_proj (read combined, W and the residual, write the
+    residual).  FLOPs: in_proj, out_proj and the slot contractions (dense C x C count).
+    Plus embedding, the two final LayerNorms and the tied head (read x and the embedding,
+    write the logits)."""
     eb = 2
     T = cfg["B"] * cfg["L"]
     dm, ds, H, C, V = cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"], 50304
     hd, P = dm // H, 3 * ds + 4 * dm
-    blk_bytes = T * eb * (2 * dm + (dm + P) + 4 * ds + 2 * dm + 5 * dm + 2 * (ds + dm) + (ds + 3 * dm)) \
+    rowln = 0 if fused_out_proj else 2 * (ds + dm)
+    blk_bytes = T * eb * (2 * dm + (dm + P) + 4 * ds + 2 * dm + 5 * dm + rowln + (ds + 3 * dm)) \
         + eb * (P * dm + dm * (ds + dm))
     blk_flops = 2 * T * dm * P + 2 * T * (ds + dm) * dm + T * H * (4 * C * hd + 4 * hd * hd)
     n = cfg["n_layers"]
@@ -250,6 +252,9 @@ def main():
     ap.add_argument("--tuned-gemms", default="on", choices=["on", "off"],
                     help="run in_proj/out_proj/LM head on the hipBLASLt/rocBLAS solutions recorded "
                          "in hdcmamba_amd/tuned/gemm_gfx950.csv (TunableOp, tuning off)")
+    ap.add_argument("--fused-out-proj", default="on", choices=["on", "off"],
+                    help="LM workloads: the LayerNorm of `combined`, out_proj and the residual add as one "
+                         "GEMM with the LayerNorm in its epilogue (on) or a row LayerNorm kernel and addmm (off)")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -274,7 +279,7 @@ def main():
     import torch
 
     from cfgs import WORKLOADS, block_input, lm_input, make_block, make_lm
-    from hdcmamba_amd import _ops
+    from hdcmamba_amd import _ops, set_fused_out_proj
     from hdcmamba_amd.gemm_tuning import use_tuned_gemms
 
     n_tuned = use_tuned_gemms() if args.tuned_gemms == "on" else 0
@@ -286,6 +291,7 @@ def main():
     cfg["dtype_name"] = "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32"
     if args.workload.startswith("lm"):
         model = make_lm(args.workload).to(cfg["dtype"]).to(dev)
+        set_fused_out_proj(model, args.fused_out_proj == "on")
         inp = lm_input(args.workload).to(dev)
         workload = (f"{cfg['n_layers']}-layer d_model={cfg['d_model']} HdcMamba LM forward, "
                     f"B={cfg['B']}, L={cfg['L']}")
@@ -311,7 +317,7 @@ def main():
         k_steps = max(1, min(args.steps, 5))
         model(inp)
         torch.cuda.synchronize()
-        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln"}
+        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln", "rowln_gemm"}
         t2 = time.perf_counter()
         for _ in range(k_steps):
             model(inp)
@@ -327,6 +333,11 @@ def main():
     kernels = {}
     for name, ms in times.items():
         us = sum(ms) / len(ms) * 1e3
+        if name == "rowln_gemm":  # MFMA-bound: out_proj's FLOPs
+            tfs = 2 * tokens * (cfg["d_state"] + cfg["d_model"]) * cfg["d_model"] / (us * 1e-6) / 1e12
+            kernels[name] = {"us": round(us, 2), "launches": len(ms), "TFLOP/s": round(tfs, 1),
+                             "frac_bf16_mfma": round(tfs / 2500.0, 4)}
+            continue
         gbs = kernel_bytes(cfg, name) * tokens / (us * 1e-6) / 1e9
         kernels[name] = {"us": round(us, 2), "launches": len(ms), "GB/s": round(gbs, 1),
                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -343,7 +354,7 @@ def main():
 
     forward_summary = None
     if args.workload.startswith("lm"):
-        fl, by = forward_totals(cfg)
+        fl, by = forward_totals(cfg, args.fused_out_proj == "on")
         sec_step = ms_per_step * 1e-3
         forward_summary = {"TFLOP": round(fl / 1e12, 2), "TFLOP/s": round(fl / sec_step / 1e12, 1),
                            "frac_bf16_mfma_peak": round(fl / sec_step / 2.5e15, 4),
@@ -363,7 +374,8 @@ def main():
         "config": {"workload": workload, "d_model": cfg["d_model"], "d_state": cfg["d_state"],
                    "num_heads": cfg["num_heads"], "chunk": cfg["chunk"], "layers": cfg.get("n_layers", 1),
                    "vocab": 50304 if args.workload.startswith("lm") else None,
-                   "global_batch": cfg["B"], "seq_len": cfg["L"], "parallelism": "none (1 GPU)"},
+                   "global_batch": cfg["B"], "seq_len": cfg["L"], "parallelism": "none (1 GPU)",
+                   "fused_out_proj": args.fused_out_proj == "on"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,

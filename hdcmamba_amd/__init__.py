@@ -9,6 +9,7 @@ from .model import (
     HdcMamba9v3Model,
     fused_norm_conv1d_trainable,
     set_differentiable_mixer,
+    set_fused_out_proj,
 )
 from .lm import DecodeGraph, ForwardGraph, HdcMambaLM
 
@@ -22,4 +23,5 @@ __all__ = [
     "DecodeGraph",
     "ForwardGraph",
     "set_differentiable_mixer",
+    "set_fused_out_proj",
 ]

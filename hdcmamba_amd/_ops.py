@@ -61,6 +61,10 @@ _PROTOS = {
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
     "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                      c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+                              c_int64, c_int, c_void_p]),
+    "hdcm_rowln_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                    c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
     "hdcm_rowln_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "hdcm_rowln_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_float, c_int, c_void_p]),
@@ -492,6 +496,62 @@ def chunk_pos_advance(pos_dev, chunk):
 # ----------------------------------------------------------------------------- decode projections
 SKINNY_MAX_ROWS = 16
 SKINNY_MAX_K = 3072
+
+
+def _rows_view(t: torch.Tensor, K: int) -> torch.Tensor:
+    """t [..., K] as a 2-D view with unit inner stride and 16-byte aligned rows (a copy if
+    the layout does not allow one)."""
+    t2 = t.reshape(-1, K)
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) % 8) or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+def gemm(x, weight, bias=None, out=None):
+    """x [..., K] @ weight[N, K]^T (+ bias[N]) -> [..., N] on the tiled bf16 MFMA GEMM (fp32
+    accumulation, one rounding).  ``out`` may be a strided [..., N] view (unit inner stride)."""
+    _on_gpu(x, weight)
+    K = x.shape[-1]
+    N = weight.shape[0]
+    lead = x.shape[:-1]
+    x2 = _rows_view(x, K)
+    M = x2.shape[0]
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if out is None:
+        out = torch.empty(*lead, N, device=x.device, dtype=x.dtype)
+    o2 = out.view(-1, N) if out.is_contiguous() else out.reshape(-1, N)
+    if bias is not None:
+        bias = _same(bias, x, "bias")
+    ev = timer.begin("gemm")
+    _check("hdcm_gemm_fwd", lib().hdcm_gemm_fwd(
+        x2.data_ptr(), x2.stride(0), w.data_ptr(), w.stride(0), bias.data_ptr() if bias is not None else None,
+        o2.data_ptr(), o2.stride(0), M, N, K, _dtype(x), _stream(x)))
+    timer.end("gemm", ev)
+    return out
+
+
+def rowln_gemm(c, weight, residual, eps=1e-5, out=None):
+    """residual + LN(c) @ weight^T, LN the row LayerNorm without affine over c's last dim;
+    the row statistics and the weight's row sums are computed inside the GEMM.  ``out`` may
+    be ``residual``."""
+    _on_gpu(c, weight, residual)
+    K = c.shape[-1]
+    N = weight.shape[0]
+    c2 = _rows_view(c, K)
+    M = c2.shape[0]
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    r2 = residual.reshape(-1, N)
+    if r2.stride(-1) != 1:
+        raise ValueError("residual must have a unit inner stride")
+    if out is None:
+        out = torch.empty(*c.shape[:-1], N, device=c.device, dtype=c.dtype)
+    o2 = out.view(-1, N) if out.is_contiguous() else out.reshape(-1, N)
+    ev = timer.begin("rowln_gemm")
+    _check("hdcm_rowln_gemm_fwd", lib().hdcm_rowln_gemm_fwd(
+        c2.data_ptr(), c2.stride(0), w.data_ptr(), w.stride(0), r2.data_ptr(), r2.stride(0), o2.data_ptr(),
+        o2.stride(0), M, N, K, float(eps), _dtype(c), _stream(c)))
+    timer.end("rowln_gemm", ev)
+    return out
 
 
 def skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:

@@ -26,7 +26,7 @@ from . import _ops
 
 __all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
            "fused_norm_conv1d_trainable", "RowLayerNormFunction", "layer_norm", "SlotSsmMixerFunction",
-           "set_differentiable_mixer", "BlockState"]
+           "set_differentiable_mixer", "set_fused_out_proj", "BlockState"]
 
 
 @dataclass
@@ -175,11 +175,17 @@ class HdcMamba9v3Block(nn.Module):
     kernels are constants for autograd.  With ``differentiable_mixer = True`` (an added
     option) the training forward runs them through SlotSsmMixerFunction instead, so
     in_proj, the LN+conv, A_log and the GroupNorm receive gradients too.
+
+    ``fused_out_proj`` (added, on by default): without autograd and in bf16, the LayerNorm
+    of `combined`, out_proj and the residual add run as one GEMM whose epilogue applies the
+    LayerNorm (hdcm_rowln_gemm_fwd); otherwise as a row LayerNorm kernel and addmm.
     """
 
-    def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False):
+    def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False,
+                 fused_out_proj=True):
         super().__init__()
         self.differentiable_mixer = differentiable_mixer
+        self.fused_out_proj = fused_out_proj
         self.d_model, self.d_state = d_model, d_state
         self.num_heads, self.chunk_size = num_heads, chunk_size
         self.head_dim = d_model // num_heads
@@ -206,10 +212,10 @@ class HdcMamba9v3Block(nn.Module):
         self.group_norm = nn.GroupNorm(num_heads, d_model)
         self.register_buffer("gamma_buf", torch.exp(-F.softplus(self.decay_log)))
 
-    def _mixer(self, x, state=None):
-        """LN+conv, in_proj, SSM and slot+gate into one `combined` row buffer, then its
-        LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm].  With ``state``,
-        the SSM and slot states after the last row are written into it."""
+    def _mixer(self, x, state=None, normalize=True):
+        """LN+conv, in_proj, SSM and slot+gate into one `combined` row buffer, then (with
+        ``normalize``) its LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm].
+        With ``state``, the SSM and slot states after the last row are written into it."""
         B, L, dm = x.shape
         ds, H, C = self.d_state, self.num_heads, self.chunk_size
         dtype = x.dtype
@@ -234,8 +240,14 @@ class HdcMamba9v3Block(nn.Module):
         main.wait_stream(side)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
                        combined, ds, dm, H, C, S_final=None if state is None else state.S_prev)
-        _ops.layer_norm(combined, eps=1e-5, out=combined)
+        if normalize:
+            _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
+
+    def _fused_out(self, x):
+        """Whether out_proj runs as the GEMM with the LayerNorm folded in (no autograd)."""
+        return (self.fused_out_proj and x.dtype == torch.bfloat16 and not torch.is_grad_enabled()
+                and (self.d_state + self.d_model) % 8 == 0 and self.d_model % 4 == 0)
 
     def _differentiable_mixer(self, x):
         """_mixer with autograd through every stage (differentiable_mixer)."""
@@ -254,6 +266,9 @@ class HdcMamba9v3Block(nn.Module):
     def _inner_forward(self, x, state=None):
         """Block body on a chunk-aligned [B,L,dm] input; returns x + out_proj(LN(combined))."""
         B, L, dm = x.shape
+        if self._fused_out(x):
+            c = self._mixer(x, state, normalize=False)
+            return _ops.rowln_gemm(c, self.out_proj.weight.to(x.dtype), x.reshape(B * L, dm)).view(B, L, dm)
         if self.differentiable_mixer and state is None and torch.is_grad_enabled():
             c = self._differentiable_mixer(x)
         else:
@@ -267,6 +282,11 @@ class HdcMamba9v3Block(nn.Module):
         B, L, dm = r.shape
         if state is not None:
             self._capture_conv(r, state)
+        if self._fused_out(r):
+            c = self._mixer(r, state, normalize=False)
+            r2 = r.view(B * L, dm)
+            _ops.rowln_gemm(c, self.out_proj.weight.to(r.dtype), r2, out=r2)
+            return r
         c = self._mixer(r, state)
         r.view(B * L, dm).addmm_(c, self.out_proj.weight.to(r.dtype).t())
         return r
@@ -409,6 +429,15 @@ class HdcMamba9v3Model(nn.Module):
             for layer, st in zip(self.layers, states):
                 x = layer.step(x, st, pos_dev)
         return _ops.layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
+
+
+def set_fused_out_proj(module, enabled=True):
+    """Switch the folded LayerNorm + out_proj GEMM of every HdcMamba9v3Block inside
+    ``module`` on or off; returns ``module``."""
+    for m in module.modules():
+        if isinstance(m, HdcMamba9v3Block):
+            m.fused_out_proj = bool(enabled)
+    return module
 
 
 def set_differentiable_mixer(module, enabled=True):

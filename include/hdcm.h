@@ -244,6 +244,29 @@ int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const void* W, int
                          void* stream);
 
 /*
+ * Tiled bf16 GEMM: out[t,o] = sum_k x[t,k] w[o,k] (+ bias[o]) for t < M, o < N, fp32
+ * accumulation, one rounding to bf16.  w is an nn.Linear weight [N,K]; bias may be NULL.
+ * Needs K % 8 == 0, N % 4 == 0, 16-byte aligned rows of x and w, 8-byte aligned out.
+ * Replaces the nn.Linear in_proj of the prefill/forward (hdcmamba/model.py:313,340).
+ */
+int hdcm_gemm_fwd(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+                  const void* bias, void* out, int64_t out_row_stride, int64_t M, int64_t N, int64_t K,
+                  int dtype, void* stream);
+
+/*
+ * out_proj over the row LayerNorm without affine, with the residual add:
+ *   out[t,o] = res[t,o] + r_t * (sum_k c[t,k] w[o,k] - mu_t * s_o),  s_o = sum_k w[o,k]
+ * which equals res + LN(c) w^T with LN(c)_t = (c_t - mu_t) r_t over the K columns of row t
+ * (mu_t the mean, r_t = 1/sqrt(var_t + eps), biased variance).  mu, r and s are computed in
+ * the kernel from the operands it multiplies.  res may alias out.  Alignment as
+ * hdcm_gemm_fwd.  Replaces F.layer_norm(combined.float(), (ds+dm,)).to(dtype), out_proj and
+ * the residual add (hdcmamba/model.py:382-383,394).
+ */
+int hdcm_rowln_gemm_fwd(const void* c, int64_t c_row_stride, const void* w, int64_t w_row_stride,
+                        const void* res, int64_t res_row_stride, void* out, int64_t out_row_stride,
+                        int64_t M, int64_t N, int64_t K, float eps, int dtype, void* stream);
+
+/*
  * Row LayerNorm over `width` columns, fp32 statistics, optional affine
  * (w, b may be NULL).  in and out may be the same buffer.
  * Replaces: F.layer_norm(combined.float(), (ds+dm,)).to(dtype)

@@ -156,6 +156,37 @@ def test_skinny_gemm_validation():
     assert f(*a) == OK
 
 
+def test_gemm_validation():
+    # hdcm_gemm_fwd(x, x_rs, w, w_rs, bias, out, o_rs, M, N, K, dtype, stream)
+    f = _ops.lib().hdcm_gemm_fwd
+    base = [P16, 1024, P16, 1024, None, P16, 4480, 300, 4480, 1024, 1, None]
+    a = list(base); a[10] = 0  # fp32 is not built
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[0] = None
+    assert f(*a) == EINVAL
+    a = list(base); a[6] = 100  # output row shorter than N
+    assert f(*a) == EINVAL
+    a = list(base); a[9] = 1020; a[1] = a[3] = 1020  # K not a multiple of 8
+    assert f(*a) == EALIGN
+    a = list(base); a[8] = 4478; a[6] = 4478  # N not a multiple of 4
+    assert f(*a) == EALIGN
+    a = list(base); a[1] = 1 << 22  # row stride beyond 32-bit tile offsets
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[7] = 0; a[0] = a[5] = None  # no rows
+    assert f(*a) == OK
+    # hdcm_rowln_gemm_fwd(c, c_rs, w, w_rs, res, r_rs, out, o_rs, M, N, K, eps, dtype, stream)
+    h = _ops.lib().hdcm_rowln_gemm_fwd
+    base = [P16, 1152, P16, 1152, P16, 1024, P16, 1024, 300, 1024, 1152, 1e-5, 1, None]
+    a = list(base); a[4] = None  # no residual
+    assert h(*a) == EINVAL
+    a = list(base); a[5] = 100  # residual row shorter than N
+    assert h(*a) == EINVAL
+    a = list(base); a[12] = 0
+    assert h(*a) == EUNSUPPORTED
+    a = list(base); a[8] = 0; a[0] = a[4] = a[6] = None
+    assert h(*a) == OK
+
+
 def test_norm_conv_bwd_validation():
     lib = _ops.lib()
     assert lib.hdcm_norm_conv_bwd_workspace_bytes(1, 32768, 1024) == 32768 * 8 + 512 * 7 * 1024 * 4  # 64-row chunks

@@ -266,6 +266,65 @@ def test_skinny_gemm_in_place_residual(dev):
     assert (err <= 2 ** -8 * ref.abs() + 1e-3).all()
 
 
+# ----------------------------------------------------------------------------- tiled GEMM
+@pytest.mark.parametrize("M,N,K,bias", [
+    (300, 100, 72, True), (100, 64, 40, False), (1000, 4480, 1024, True), (257, 260, 1152, False),
+    (513, 4480, 1000, True), (700, 512, 160, True), (1, 8, 8, True), (256, 256, 64, False),
+])
+def test_tiled_gemm(dev, M, N, K, bias):
+    """hdcm_gemm_fwd against torch fp32 on the same bf16 operands: partial tiles in every
+    dimension (M, N not multiples of 256, K not a multiple of 64) and the bias epilogue."""
+    _say("gemm", M, N, K, bias)
+    g = torch.Generator().manual_seed(M + 3 * N + 7 * K)
+    X = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16) if bias else None
+    ref = X.float() @ W.float().t() + (b.float() if bias else 0.0)
+    out = _ops.gemm(X.to(dev), W.to(dev), None if b is None else b.to(dev))
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 1e-3).all(), f"max err {err.max().item()}"
+
+
+@pytest.mark.parametrize("M,N,K,mean", [
+    (300, 100, 72, 0.3), (257, 260, 1152, 4.0), (4096, 1024, 1152, 0.0), (513, 768, 832, 2.0), (1, 8, 8, 1.0),
+])
+def test_rowln_gemm(dev, M, N, K, mean):
+    """hdcm_rowln_gemm_fwd = res + LayerNorm(c) W^T (no affine, eps 1e-5) against torch fp32
+    (F.layer_norm on the bf16 rows): rows with a large mean, ragged tiles; then in place."""
+    _say("rowln_gemm", M, N, K, mean)
+    g = torch.Generator().manual_seed(M + N + K)
+    c = (1.5 * torch.randn(M, K, generator=g) + mean).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    ref = r.float() + torch.nn.functional.layer_norm(c.float(), (K,), eps=1e-5) @ W.float().t()
+    cd, Wd, rd = c.to(dev), W.to(dev), r.to(dev)
+    out = _ops.rowln_gemm(cd, Wd, rd)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
+    _ops.rowln_gemm(cd, Wd, rd, out=rd)  # out aliasing the residual
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), out.cpu())
+
+
+def test_fused_out_proj_matches_unfused(dev):
+    """A bf16 model forward with the LayerNorm folded into out_proj against the same model
+    with the row LayerNorm kernel and addmm."""
+    from hdcmamba_amd import HdcMamba9v3Model, set_fused_out_proj
+
+    torch.manual_seed(0)
+    m = HdcMamba9v3Model(256, 2, 64, 32, num_heads=4, chunk_size=64).to(torch.bfloat16).to(dev).eval()
+    x = torch.randn(2, 200, 256, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        a = m(x)
+        set_fused_out_proj(m, False)
+        b = m(x)
+    err = ((a.float() - b.float()).norm() / b.float().norm()).item()
+    _say(f"  fused vs unfused normwise {err:.2e}")
+    assert err < 1e-2
+
+
 # ----------------------------------------------------------------------------- norm_conv backward
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,L,D", [(2, 1, 256), (2, 5, 256), (1, 300, 1024), (2, 700, 768), (1, 64, 2048),
