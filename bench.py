@@ -192,6 +192,8 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
     steps = args.steps if args.steps != 10 else 128
     warm = max(args.warmup, 2)
     lm = make_lm("lm_c5").to(torch.bfloat16).to(dev)
+    from hdcmamba_amd import set_fused_out_proj
+    set_fused_out_proj(lm, args.fused_out_proj == "on")
     ids = lm_input("lm_c5", B=B, L=L + warm + steps + 1).to(dev)
     with torch.no_grad():
         lm.prefill(ids[:, :256])  # warm the prefill kernels and GEMM handles
@@ -226,7 +228,8 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
         "dtype": "bf16", "data": "synthetic: uniform random token ids, random-init weights",
         "config": {"workload": "48-layer d_model=2048 HdcMamba LM, prefill B=16 L=8192 then single-token decode",
                    "d_model": 2048, "d_state": 128, "num_heads": 32, "chunk": 64, "layers": 48, "vocab": 50304,
-                   "global_batch": B, "prefill_len": L, "graph": not args.eager},
+                   "global_batch": B, "prefill_len": L, "graph": not args.eager,
+                   "fused_out_proj": args.fused_out_proj == "on"},
         "roofline": {"kernel": "whole decode step", "bound": "hbm", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": param_bytes + state_bytes},

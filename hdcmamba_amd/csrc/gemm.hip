@@ -294,6 +294,11 @@ int check_common(const void* x, int64_t x_rs, const void* w, int64_t w_rs, const
 
 }  // namespace
 
+// skinny.hip: the row-LayerNorm fold on the decode-step kernels (M <= 16)
+bool hdcm_skinny_rowln_ok(int64_t M, int64_t K);
+int hdcm_skinny_rowln(const void* c, int64_t c_rs, const void* W, int64_t w_rs, const void* res, int64_t r_rs,
+                      void* out, int64_t o_rs, int64_t M, int64_t N, int64_t K, float eps, hipStream_t s);
+
 extern "C" int hdcm_gemm_fwd(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
                              const void* bias, void* out, int64_t out_row_stride, int64_t M, int64_t N, int64_t K,
                              int dtype, void* stream) {
@@ -320,6 +325,9 @@ extern "C" int hdcm_rowln_gemm_fwd(const void* c, int64_t c_row_stride, const vo
   HDCM_CHECK_ARG(M == 0 || res_row_stride >= N, HDCM_EINVAL);
   HDCM_CHECK_ARG(res_row_stride % 4 == 0 && ((uintptr_t)res & 7u) == 0, HDCM_EALIGN);
   if (M == 0) return HDCM_OK;
+  if (hdcm_skinny_rowln_ok(M, K))  // a few rows (decode steps): the weight-streaming kernels
+    return hdcm_skinny_rowln(c, c_row_stride, w, w_row_stride, res, res_row_stride, out, out_row_stride, M, N, K,
+                             eps, (hipStream_t)stream);
   const int64_t n_ot = (N + kBO - 1) / kBO, n_tt = (M + kBT - 1) / kBT;
   hipLaunchKernelGGL((gemm_bt_kernel<EPI_ROWLN, false>), dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const bf16_t*)c, c_row_stride, (const bf16_t*)w, w_row_stride,

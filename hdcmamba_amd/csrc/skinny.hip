@@ -24,12 +24,55 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxSteps = 24;  // K=32 steps per wave: K <= 4 * 24 * 32 = 3072
 
-template <int STEPS, bool BIAS, bool RES>
+// Row LayerNorm folded in (LN): out = res + r_m (acc - mu_m s_n), LN(c) W^T written through
+// the sums of the operands the MFMAs read: lane (l16, g) adds its A fragment's sum c and sum
+// c^2 (row m = l16) and its B fragment's sum w (column n = l16) with v_dot2_f32_bf16; the
+// four lane groups are added on lane moves and the waves' K ranges in LDS.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ln_sums(const Frag<bf16_t>& a, const Frag<bf16_t>& b, float& c1, float& c2,
+                                        float& w1) {
+  const bf16x2_t ones = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+  const uint4 ua = __builtin_bit_cast(uint4, a.v), ub = __builtin_bit_cast(uint4, b.v);
+  const unsigned da[4] = {ua.x, ua.y, ua.z, ua.w}, db[4] = {ub.x, ub.y, ub.z, ub.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const bf16x2_t p = __builtin_bit_cast(bf16x2_t, da[e]);
+    c1 = __builtin_amdgcn_fdot2_f32_bf16(p, ones, c1, false);
+    c2 = __builtin_amdgcn_fdot2_f32_bf16(p, p, c2, false);
+    w1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, db[e]), ones, w1, false);
+  }
+}
+__device__ __forceinline__ void ln_store(float (&st)[16][3], int l16, int g, float c1, float c2, float w1) {
+  c1 = quad_group_sum(c1);
+  c2 = quad_group_sum(c2);
+  w1 = quad_group_sum(w1);
+  if (g == 0) {
+    st[l16][0] = c1;
+    st[l16][1] = c2;
+    st[l16][2] = w1;
+  }
+}
+template <int NW>
+__device__ __forceinline__ float ln_apply(const float (&st)[NW][16][3], int m, int nn, int K, float eps, float acc) {
+  float s1 = 0.f, s2 = 0.f, sw = 0.f;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    s1 += st[k][m][0];
+    s2 += st[k][m][1];
+    sw += st[k][nn][2];
+  }
+  const float mu = s1 / (float)K;
+  const float r = rsqrtf(fmaxf(s2 / (float)K - mu * mu, 0.f) + eps);
+  return r * (acc - mu * sw);
+}
+
+template <int STEPS, bool BIAS, bool RES, bool LN = false>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
     const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
     const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
-    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K) {
+    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K, float eps = 0.f) {
   __shared__ float part[kWaves][16][17];
+  __shared__ float lnst[LN ? kWaves : 1][16][3];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
@@ -59,6 +102,13 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
 #pragma unroll
   for (int s = 0; s < STEPS; ++s)
     if (s < my) acc = mma(fa[s], bw[s], acc);
+  if constexpr (LN) {
+    float c1 = 0.f, c2 = 0.f, w1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+      if (s < my) ln_sums(fa[s], bw[s], c1, c2, w1);
+    ln_store(lnst[w], l16, g, c1, c2, w1);
+  }
   // D layout: lane holds D[4 g + r][l16]
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
@@ -70,6 +120,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
       const int m = 4 * g + r;
       float v = part[0][m][l16] + part[1][m][l16] + part[2][m][l16] + part[3][m][l16];
       if (m < M && n < N) {
+        if constexpr (LN) v = ln_apply<kWaves>(lnst, m, l16, K, eps, v);
         if (BIAS) v += bf2f(bias[n]);
         if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
         out[(int64_t)m * o_rs + n] = f2bf(v);
@@ -89,14 +140,15 @@ constexpr int kLdsWaves = 8;
 constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kWideN = 2048;
 
-template <int STEPS, bool BIAS, bool RES>
+template <int STEPS, bool BIAS, bool RES, bool LN = false>
 __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
     const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
     const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
-    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K) {
+    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K, float eps = 0.f) {
   constexpr int PITCH = STEPS * 32 + 8;  // slab row pitch (elements): +16 bytes staggers the banks
   __shared__ __attribute__((aligned(16))) bf16_t slab[kLdsWaves][16 * PITCH];
   __shared__ float part[kLdsWaves][16][17];
+  __shared__ float lnst[LN ? kLdsWaves : 1][16][3];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16;
@@ -129,14 +181,17 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   }
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  float c1 = 0.f, c2 = 0.f, w1 = 0.f;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     if (s < my) {
       Frag<bf16_t> b;
       b.v = *reinterpret_cast<const bf16x8_t*>(sl + l16 * PITCH + 32 * s + 8 * g);
       acc = mma(fa[s], b, acc);
+      if constexpr (LN) ln_sums(fa[s], b, c1, c2, w1);
     }
   }
+  if constexpr (LN) ln_store(lnst[w], l16, g, c1, c2, w1);
   // D layout: lane holds D[4 g + r][l16]
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
@@ -147,6 +202,7 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
 #pragma unroll
     for (int k = 0; k < kLdsWaves; ++k) v += part[k][m][nn];
     if (m < M && n < N) {
+      if constexpr (LN) v = ln_apply<kLdsWaves>(lnst, m, nn, K, eps, v);
       if (BIAS) v += bf2f(bias[n]);
       if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
       out[(int64_t)m * o_rs + n] = f2bf(v);
@@ -194,7 +250,45 @@ void launch_steps(const void* A, int64_t a_rs, const void* W, int64_t w_rs, cons
                        w_rs, bs, rs, r_rs, o, o_rs, M, N, K);
 }
 
+template <int STEPS, bool WIDE>
+void launch_ln(const bf16_t* c, int64_t c_rs, const bf16_t* W, int64_t w_rs, const bf16_t* res, int64_t r_rs,
+               bf16_t* out, int64_t o_rs, int M, int N, int K, float eps, hipStream_t s) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  if constexpr (WIDE)
+    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
+                       w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
+  else
+    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, true, true>), grid, dim3(kThreads), 0, s, c, c_rs, W,
+                       w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
+}
+
 }  // namespace
+
+// out = res + LN(c) W^T (row LayerNorm without affine over K) for M <= 16 rows: the skinny
+// kernels with the fold above.  Called by hdcm_rowln_gemm_fwd after its argument checks.
+bool hdcm_skinny_rowln_ok(int64_t M, int64_t K) {
+  return M <= 16 && K % 32 == 0 && K <= (int64_t)kWaves * kMaxSteps * 32;
+}
+int hdcm_skinny_rowln(const void* c, int64_t c_rs, const void* W, int64_t w_rs, const void* res, int64_t r_rs,
+                      void* out, int64_t o_rs, int64_t M, int64_t N, int64_t K, float eps, hipStream_t s) {
+  const bool wide = N >= kWideN;
+  const int steps = wide ? (int)((K / 32 + kLdsWaves - 1) / kLdsWaves) : (int)((K / 32 + kWaves - 1) / kWaves);
+  const bf16_t *cc = (const bf16_t*)c, *ww = (const bf16_t*)W, *rr = (const bf16_t*)res;
+  bf16_t* o = (bf16_t*)out;
+  const int m = (int)M, n = (int)N, k = (int)K;
+  if (wide) {
+    if (steps <= 4) launch_ln<4, true>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else if (steps <= 8) launch_ln<8, true>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else if (steps <= 9) launch_ln<9, true>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else launch_ln<12, true>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+  } else {
+    if (steps <= 8) launch_ln<8, false>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else if (steps <= 12) launch_ln<12, false>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else if (steps <= 18) launch_ln<18, false>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+    else launch_ln<kMaxSteps, false>(cc, c_rs, ww, w_rs, rr, r_rs, o, o_rs, m, n, k, eps, s);
+  }
+  return hdcm_launch_status();
+}
 
 extern "C" int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const void* W, int64_t w_row_stride,
                                     const void* bias, const void* res, int64_t res_row_stride, void* out,

@@ -178,7 +178,8 @@ class HdcMamba9v3Block(nn.Module):
 
     ``fused_out_proj`` (added, on by default): without autograd and in bf16, the LayerNorm
     of `combined`, out_proj and the residual add run as one GEMM whose epilogue applies the
-    LayerNorm (hdcm_rowln_gemm_fwd); otherwise as a row LayerNorm kernel and addmm.
+    LayerNorm (hdcm_rowln_gemm_fwd) at the shapes where that measured faster (see
+    ``_fused_out``); otherwise as a row LayerNorm kernel and addmm.
     """
 
     def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False,
@@ -245,9 +246,17 @@ class HdcMamba9v3Block(nn.Module):
         return combined.view(B * L, ds + dm)
 
     def _fused_out(self, x):
-        """Whether out_proj runs as the GEMM with the LayerNorm folded in (no autograd)."""
-        return (self.fused_out_proj and x.dtype == torch.bfloat16 and not torch.is_grad_enabled()
-                and (self.d_state + self.d_model) % 8 == 0 and self.d_model % 4 == 0)
+        """Whether out_proj runs as the GEMM with the LayerNorm folded in (bf16, no autograd).
+        Measured: it pays on the decode step (<= 16 rows: the weight-streaming kernels) and
+        up to ~1024 output tiles of 256 x 256 (the 32768-token d_model=1024 forward: 512);
+        at the 131072-token d_model=2048 prefill (4096 tiles) hipBLASLt's out_proj plus the
+        LayerNorm kernel is ~5 % faster than the tiled GEMM, so that shape keeps them."""
+        if not (self.fused_out_proj and x.dtype == torch.bfloat16 and not torch.is_grad_enabled()
+                and (self.d_state + self.d_model) % 8 == 0 and self.d_model % 4 == 0):
+            return False
+        rows = x.numel() // self.d_model
+        tiles = -(-rows // 256) * -(-self.d_model // 256)
+        return rows <= 16 or tiles <= 1024
 
     def _differentiable_mixer(self, x):
         """_mixer with autograd through every stage (differentiable_mixer)."""
@@ -337,12 +346,15 @@ class HdcMamba9v3Block(nn.Module):
         _ops.mixer_step(projs, self.A_log, ds, 3 * ds, self.gamma_buf.to(dtype), self.group_norm.weight,
                         self.group_norm.bias, 1e-5, state.h, state.S_prev, state.S_intra, state.pos, C,
                         combined, dm, H, pos_dev=pos_dev)
-        _ops.layer_norm(combined, eps=1e-5, out=combined)
         w_out = self.out_proj.weight.to(dtype)
-        if _ops.skinny_ok(combined, w_out):
-            y = _ops.skinny_linear(combined, w_out, residual=x)
+        if self._fused_out(x):  # LayerNorm folded into the (skinny) out_proj GEMM
+            y = _ops.rowln_gemm(combined, w_out, x)
         else:
-            y = torch.addmm(x, combined, w_out.t())
+            _ops.layer_norm(combined, eps=1e-5, out=combined)
+            if _ops.skinny_ok(combined, w_out):
+                y = _ops.skinny_linear(combined, w_out, residual=x)
+            else:
+                y = torch.addmm(x, combined, w_out.t())
         if pos_dev is None:
             state.pos = (state.pos + 1) % C
         return y

@@ -288,10 +288,13 @@ def test_tiled_gemm(dev, M, N, K, bias):
 
 @pytest.mark.parametrize("M,N,K,mean", [
     (300, 100, 72, 0.3), (257, 260, 1152, 4.0), (4096, 1024, 1152, 0.0), (513, 768, 832, 2.0), (1, 8, 8, 1.0),
+    # at most 16 rows and K a multiple of 32: the decode-step (skinny) kernels, narrow and wide
+    (16, 1024, 1152, 3.0), (7, 768, 832, 0.5), (16, 2048, 2176, 1.0), (1, 2052, 64, 2.0), (3, 100, 3072, 0.0),
 ])
 def test_rowln_gemm(dev, M, N, K, mean):
     """hdcm_rowln_gemm_fwd = res + LayerNorm(c) W^T (no affine, eps 1e-5) against torch fp32
-    (F.layer_norm on the bf16 rows): rows with a large mean, ragged tiles; then in place."""
+    (F.layer_norm on the bf16 rows): rows with a large mean, ragged tiles, the few-row
+    decode shapes; then in place."""
     _say("rowln_gemm", M, N, K, mean)
     g = torch.Generator().manual_seed(M + N + K)
     c = (1.5 * torch.randn(M, K, generator=g) + mean).to(torch.bfloat16)
