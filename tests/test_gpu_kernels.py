@@ -230,6 +230,9 @@ def test_slot_unsupported_head_dim(dev):
     (3, 2048, 64, True, True),
     (9, 2050, 1024, False, True),
     (16, 4096, 3072, True, False),
+    # more than 384 tiles with K <= 2048: two tiles per workgroup (odd tile count: the last
+    # workgroup's second tile lies past N)
+    (16, 8576, 2048, True, False), (5, 6210, 512, False, True),
 ])
 def test_skinny_gemm(dev, M, N, K, bias, res):
     """bf16 operands, fp32 accumulation, one rounding: against torch fp32 on the same
