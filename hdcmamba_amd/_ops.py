@@ -519,7 +519,7 @@ def gemm(x, weight, bias=None, out=None):
     w = weight if weight.is_contiguous() else weight.contiguous()
     if out is None:
         out = torch.empty(*lead, N, device=x.device, dtype=x.dtype)
-    o2 = out.view(-1, N) if out.is_contiguous() else out.reshape(-1, N)
+    o2 = out.view(-1, N)  # a view (never a copy): the kernel writes through it
     if bias is not None:
         bias = _same(bias, x, "bias")
     ev = timer.begin("gemm")
@@ -545,7 +545,7 @@ def rowln_gemm(c, weight, residual, eps=1e-5, out=None):
         raise ValueError("residual must have a unit inner stride")
     if out is None:
         out = torch.empty(*c.shape[:-1], N, device=c.device, dtype=c.dtype)
-    o2 = out.view(-1, N) if out.is_contiguous() else out.reshape(-1, N)
+    o2 = out.view(-1, N)  # a view (never a copy): the kernel writes through it
     ev = timer.begin("rowln_gemm")
     _check("hdcm_rowln_gemm_fwd", lib().hdcm_rowln_gemm_fwd(
         c2.data_ptr(), c2.stride(0), w.data_ptr(), w.stride(0), r2.data_ptr(), r2.stride(0), o2.data_ptr(),
