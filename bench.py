@@ -9,7 +9,7 @@ with tokens/s, the roofline of the dominant custom kernel (HIP events on the lau
 around each custom kernel, over a second timed region of eager forwards), per-kernel
 figures, and the CPU oracle's throughput on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2|lm_c5_decode]
+    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2|lm_c5_decode|lm_c4_train]
                     [--graph on|off] [--tuned-gemms on|off] [--cpu-baseline on|off]
 """
 from __future__ import annotations
@@ -239,12 +239,64 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
     print(json.dumps(out), flush=True)
 
 
+def train_bench(args, torch, cfg, make_lm, lm_input, dev):
+    """Training steps of the headline LM as the reference's trainer runs them
+    (train_fineweb.py:161-179): bf16 model under autocast, cross-entropy on fp32 logits,
+    backward, AdamW step.  `--differentiable-mixer` also trains in_proj, the LN+conv, A_log
+    and the GroupNorm (the reference's kernels have no backward)."""
+    import torch.nn.functional as F
+    from hdcmamba_amd import set_differentiable_mixer
+
+    L = cfg["L"]
+    steps = args.steps if args.steps != 10 else 3
+    warm = max(args.warmup if args.warmup != 3 else 2, 1)
+    lm = make_lm("lm_c4").to(torch.bfloat16).to(dev).train()
+    set_differentiable_mixer(lm, args.differentiable_mixer)
+    opt = torch.optim.AdamW(lm.parameters(), lr=1e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    ids = lm_input("lm_c4", B=cfg["B"], L=L + 1).to(dev)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        with torch.amp.autocast("cuda", dtype=torch.bfloat16):
+            logits = lm(ids[:, :-1])
+            loss = F.cross_entropy(logits.view(-1, logits.size(-1)).float(), ids[:, 1:].reshape(-1))
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(warm):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    tokens = cfg["B"] * L * steps
+    out = {
+        "metric": "training tokens/sec on 1 MI355X at L=32768 (forward, loss, backward, AdamW)",
+        "value": round(tokens / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(sec / steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic: uniform random token ids, random-init weights",
+        "config": {"workload": "24-layer d_model=1024 HdcMamba LM training step, B=1, L=32768",
+                   "differentiable_mixer": bool(args.differentiable_mixer), "optimizer": "AdamW",
+                   "loss": "cross-entropy on fp32 logits (train_fineweb.py:170-171)"},
+        "loss": round(float(loss), 4),
+        "peak_memory_GiB": round(torch.cuda.max_memory_allocated() / 2 ** 30, 1),
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="lm_c4", choices=["lm_c4", "lm_c3", "block_c2", "lm_c5_decode"],
+    ap.add_argument("--differentiable-mixer", action="store_true",
+                    help="lm_c4_train: train the SSM, slot and gate parameters too")
+    ap.add_argument("--workload", default="lm_c4",
+                    choices=["lm_c4", "lm_c3", "block_c2", "lm_c5_decode", "lm_c4_train"],
                     help="lm_c5_decode: 48-layer d_model=2048 LM, prefill B=16 x 8192, then timed "
                          "single-token decode steps (a separate measurement, not the headline line)")
     ap.add_argument("--eager", action="store_true", help="lm_c5_decode: step from Python instead of "
@@ -290,6 +342,8 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload == "lm_c5_decode":
         return decode_bench(args, torch, WORKLOADS["lm_c5"], make_lm, lm_input, dev)
+    if args.workload == "lm_c4_train":
+        return train_bench(args, torch, WORKLOADS["lm_c4"], make_lm, lm_input, dev)
     cfg = dict(WORKLOADS[args.workload])
     cfg["dtype_name"] = "bf16" if cfg["dtype"] == torch.bfloat16 else "fp32"
     if args.workload.startswith("lm"):
