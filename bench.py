@@ -403,6 +403,15 @@ def main():
     roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": d["frac_hbm"], "traffic": stored_traffic(args.workload),
                 "bytes_per_launch": kernel_bytes(cfg, dom) * tokens}
+    # the fused out_proj (LayerNorm folded into the GEMM) is the largest kernel of this build by
+    # time; it is MFMA-bound, so its roofline is FLOPs against the bf16 dense peak
+    roofline_out_proj = None
+    if "rowln_gemm" in kernels:
+        k = kernels["rowln_gemm"]
+        fl = 2 * tokens * (cfg["d_state"] + cfg["d_model"]) * cfg["d_model"]
+        roofline_out_proj = {"kernel": "rowln_gemm (out_proj with the folded LayerNorm and the residual)",
+                             "bound": "mfma", "achieved": k["TFLOP/s"], "peak": 2500.0, "unit": "TFLOP/s",
+                             "frac": k["frac_bf16_mfma"], "traffic": None, "flops_per_launch": fl}
     if "slot_state" in kernels:
         us = kernels["slot_state"]["us"] + kernels["slot_gate"]["us"]
         gbs = kernel_bytes(cfg, "slot_gate") * tokens / (us * 1e-6) / 1e9
@@ -434,6 +443,7 @@ def main():
                    "global_batch": cfg["B"], "seq_len": cfg["L"], "parallelism": "none (1 GPU)",
                    "fused_out_proj": args.fused_out_proj == "on"},
         "roofline": roofline,
+        "roofline_out_proj": roofline_out_proj,
         "cpu_baseline": cpu,
         "kernels": kernels,
         "forward": forward_summary,
