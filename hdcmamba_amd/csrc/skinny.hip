@@ -13,7 +13,8 @@
 //     wave reads its K range of the 16 rows row-major (a few hundred contiguous bytes of a
 //     row per instruction) into a private LDS slab and takes the fragments from there.
 // A (the 16 activation rows, a few tens of KB) is read from L2.  The partial 16x16 tiles are
-// summed through LDS and the epilogue adds bias and residual in fp32 and rounds once to bf16.
+// summed through LDS and the epilogue adds bias and residual (loaded at the start, so no load
+// waits behind the MFMAs) in fp32 and rounds once to bf16.
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -87,6 +88,18 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
   // N-1 (their outputs are not stored).  Every load of the wave is issued before the first
   // MFMA (A first: it is L2-resident and returns ahead of W), so the wave waits for one
   // memory round trip instead of one per K step.
+  // the epilogue's bias and residual values, loaded now so the epilogue waits for nothing
+  float pre[4] = {0.f, 0.f, 0.f, 0.f};
+  if (w == 0 && n0 + l16 < N) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * g + r;
+      if (m < M) {
+        if (BIAS) pre[r] += bf2f(bias[n0 + l16]);
+        if (RES) pre[r] += bf2f(res[(int64_t)m * r_rs + n0 + l16]);
+      }
+    }
+  }
   const int am = l16 < M ? l16 : 0;
   const bf16_t* ap = A + (int64_t)am * a_rs + 8 * g;
   const int wn = min(n0 + l16, N - 1);
@@ -121,9 +134,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
       float v = part[0][m][l16] + part[1][m][l16] + part[2][m][l16] + part[3][m][l16];
       if (m < M && n < N) {
         if constexpr (LN) v = ln_apply<kWaves>(lnst, m, l16, K, eps, v);
-        if (BIAS) v += bf2f(bias[n]);
-        if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
-        out[(int64_t)m * o_rs + n] = f2bf(v);
+        out[(int64_t)m * o_rs + n] = f2bf(v + pre[r]);
       }
     }
   }
@@ -159,6 +170,12 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   // the K step a slot s < STEPS of this wave reads: its own, or (past its range) one inside the row
   auto step_of = [&](int s) { return min(s0 + max(min(s, my - 1), 0), nsteps - 1); };
 
+  // the epilogue's bias and residual value, loaded now so the epilogue waits for nothing
+  float pre = 0.f;
+  if (tid < 256 && tid / 16 < M && n0 + tid % 16 < N) {
+    if (BIAS) pre += bf2f(bias[n0 + tid % 16]);
+    if (RES) pre += bf2f(res[(int64_t)(tid / 16) * r_rs + n0 + tid % 16]);
+  }
   uint4 raw[STEPS];
 #pragma unroll
   for (int i = 0; i < STEPS; ++i) {
@@ -203,9 +220,7 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
     for (int k = 0; k < kLdsWaves; ++k) v += part[k][m][nn];
     if (m < M && n < N) {
       if constexpr (LN) v = ln_apply<kLdsWaves>(lnst, m, nn, K, eps, v);
-      if (BIAS) v += bf2f(bias[n]);
-      if (RES) v += bf2f(res[(int64_t)m * r_rs + n]);
-      out[(int64_t)m * o_rs + n] = f2bf(v);
+      out[(int64_t)m * o_rs + n] = f2bf(v + pre);
     }
   }
 }
