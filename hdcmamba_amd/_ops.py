@@ -47,8 +47,8 @@ _PROTOS = {
                                    c_void_p, c_size_t, c_void_p, c_int64, c_int64, c_void_p,
                                    c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_slot_attend_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p,
-                                     c_size_t, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
-                                     c_int64, c_int, c_void_p]),
+                                     c_size_t, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
+                                     c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_rowln_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                c_int64, c_float, c_int, c_void_p]),
     "hdcm_norm_conv_step_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
@@ -345,26 +345,35 @@ def slot_state(projs, q_col, gamma, d_model, num_heads, chunk, ws, S0=None):
 
 
 def slot_attend(base, q_col, k_col, v_col, gamma, d_model, num_heads, chunk, phi, out, out_col, reverse=False,
-                ws=None):
+                ws=None, chain=None):
     """Slot recurrence without GroupNorm/gate on column blocks of base [B,L,W] into
-    out[..., out_col:out_col+d_model]; ``reverse`` walks every sequence from its last token."""
+    out[..., out_col:out_col+d_model]; ``reverse`` walks every sequence from its last token.
+    With ``chain`` ([B,L,W'] in out's column layout) each output is multiplied by phi'(z), z
+    the value of chain at the output's row and column."""
     _on_gpu(base, out)
     B, L, _ = base.shape
     if out.dtype != base.dtype or out.shape[:2] != base.shape[:2]:
         raise RuntimeError("slot_attend: out must match base in dtype and [B, L]")
+    if chain is not None and (chain.dtype != out.dtype or chain.shape[:2] != out.shape[:2]):
+        raise RuntimeError("slot_attend: chain must match out in dtype and [B, L]")
     gamma = _same(gamma, base, "gamma")
     if ws is None:
         ws = slot_workspace(base, d_model, num_heads, chunk)
     brs, ors = _rows2d(base, "base"), _rows2d(out, "out")
     bptr, optr = base.data_ptr(), out.data_ptr()
+    zrs = _rows2d(chain, "chain") if chain is not None else 0
+    zptr = chain.data_ptr() if chain is not None else None
     if reverse and B * L > 0:  # start at the last row; negative row strides
         bptr += (B * L - 1) * brs * base.element_size()
         optr += (B * L - 1) * ors * out.element_size()
         brs, ors = -brs, -ors
+        if chain is not None:
+            zptr += (B * L - 1) * zrs * chain.element_size()
+            zrs = -zrs
     ev = timer.begin("slot_attend")
     _check("hdcm_slot_attend_fwd", lib().hdcm_slot_attend_fwd(
         bptr, brs, q_col, k_col, v_col, gamma.data_ptr(), 1 if phi else 0, ws.data_ptr(), ws.numel(), optr, ors,
-        out_col, B, L, d_model, num_heads, chunk, _dtype(base), _stream(base)))
+        out_col, zptr, zrs, B, L, d_model, num_heads, chunk, _dtype(base), _stream(base)))
     timer.end("slot_attend", ev)
     return out
 

@@ -304,14 +304,16 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
 }
 
 // PHI: feature map phi on q and k (else the identity).  EPI: GroupNorm + sigmoid gate
-// epilogue (else y itself is stored).  k, v and the gate start k_off, v_off, g_off columns
-// after q in each row.
-template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI>
+// epilogue (else y itself is stored).  CHAIN (without EPI): each stored value is multiplied by
+// phi'(z) = 1 (z > 0) else exp(z), z read from zb at the output's own row and column (zb has
+// the output's column layout, row stride zrs) — the feature map's chain rule of a gradient
+// pass.  k, v and the gate start k_off, v_off, g_off columns after q in each row.
+template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI, bool CHAIN = false>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int k_off, int v_off, int g_off, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
-    int64_t ors, int out_col, float* __restrict__ S_final) {
+    int64_t ors, int out_col, float* __restrict__ S_final, const T* __restrict__ zb = nullptr, int64_t zrs = 0) {
   using LD = Lds<T, HD, TC>;
   using TL = TileLoader<T, HD, TC, 0, 3>;
   static_assert(LD::total * sizeof(T) + 2 * HD * sizeof(float) <= 160 * 1024, "LDS budget");
@@ -333,7 +335,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   const int p_begin = seg * seg_tiles * TC;
   const int p_end = min(L, p_begin + seg_tiles * TC);
   const T* colbase = projs + q_col + h * HD;
-  const T* gatebase = colbase + g_off;
+  // the gate (EPI), or the chain rule's z (CHAIN: same positions as the output)
+  const T* gatebase = CHAIN ? zb + out_col + h * HD : colbase + g_off;
+  const int64_t grs = CHAIN ? zrs : prs;
 
   if (EPI && tid < HD) {
     sgw[tid] = to_f<T>(gn_w[h * HD + tid]);
@@ -379,11 +383,11 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   const int giq = (w < NIT ? w : 0) * 16 + l16;
   auto load_gate = [&](int pt) {
     const int tl = min(TC, L - pt);
-    const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * prs + gcol;
+    const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * grs + gcol;
 #pragma unroll
     for (int g = 0; g < NG; ++g) graw[g] = *reinterpret_cast<const uint4*>(grow + g * gstep);
   };
-  if (EPI && w < NIT) load_gate(p_begin);
+  if ((EPI || CHAIN) && w < NIT) load_gate(p_begin);
 
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);
@@ -548,7 +552,18 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           }
           const auto s0 = __builtin_amdgcn_permlane16_swap(ow[0][0], ow[1][0], false, false);
           const auto s1 = __builtin_amdgcn_permlane16_swap(ow[0][1], ow[1][1], false, false);
-          if (iq < tlen) *reinterpret_cast<uint4*>(orow + pp * 32) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+          uint4 ov = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+          if constexpr (CHAIN) {  // 8 consecutive columns; z was loaded with them, a tile ahead
+            {
+              float zf[8], of[8];
+              unpack16<T>(graw[pp], zf);
+              unpack16<T>(ov, of);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) of[e] *= zf[e] > 0.f ? 1.0f : fexp(zf[e]);
+              ov = __builtin_bit_cast(uint4, pack_bf16x8(of));
+            }
+          }
+          if (iq < tlen) *reinterpret_cast<uint4*>(orow + pp * 32) = ov;
         }
       } else if (iq < tlen) {
         T* orow = out + (rowbase + p + iq) * ors + out_col + h * HD + kg * 4;
@@ -558,11 +573,17 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           if constexpr (EPI) load4<T>(reinterpret_cast<const T*>(&graw[vt]), gv);
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = out_val(vt, r, gv[r]);
+          if constexpr (CHAIN) {
+            float z[4];
+            load4<T>(reinterpret_cast<const T*>(&graw[vt]), z);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] *= z[r] > 0.f ? 1.0f : fexp(z[r]);
+          }
           store4<T>(orow + vt * 16, o);
         }
       }
       // next tile's gate (this tile's again after the last: a fixed load count)
-      if constexpr (EPI) load_gate(p + TC < p_end ? p + TC : p);
+      if constexpr (EPI || CHAIN) load_gate(p + TC < p_end ? p + TC : p);
     }
 
     // ---- state update: (W or A) <- gamma^tlen * (W or A) + K~^T V
@@ -819,22 +840,24 @@ int launch_state(const void* base, int64_t prs, int64_t k_col, int64_t v_off, co
 }
 
 // q at column q_col of each row; k, v and the gate k_off, v_off, g_off columns after q.
-template <typename T, int HD, bool PHI, bool EPI>
+template <typename T, int HD, bool PHI, bool EPI, bool CHAIN = false>
 int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int64_t v_off, int64_t g_off,
                 const void* gamma, const void* gn_w, const void* gn_b, float gn_eps, const void* ws, void* out,
                 int64_t ors, int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t H, int64_t C,
-                const SlotPlan& pl, hipStream_t s) {
+                const SlotPlan& pl, hipStream_t s, const void* zb = nullptr, int64_t zrs = 0) {
   constexpr int TC = TileOf<T>::value;
   const float* Ain = (const float*)ws + (size_t)B * H * pl.nseg * HD * HD;
   // heads vary fastest so the workgroups that run together read the same rows of projs
   dim3 grid((unsigned)H, pl.nseg, (unsigned)B);
   // 16-byte output runs need 16-byte aligned rows and columns (bf16 only; fp32 always has them)
-  const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0;
+  // (with CHAIN the z rows must allow the same 16-byte runs)
+  const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0 &&
+                     (!CHAIN || (((uintptr_t)zb % 16) == 0 && zrs % 8 == 0));
 #define HDCM_GATE_LAUNCH(W, P)                                                                              \
-  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI>), grid, dim3(kThreads), 0, s,           \
+  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
                      (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
                      pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, \
-                     pl.nseg, (T*)out, ors, (int)out_col, S_final)
+                     pl.nseg, (T*)out, ors, (int)out_col, S_final, (const T*)zb, zrs)
   if (pl.has_w) {
     if (pairs) HDCM_GATE_LAUNCH(true, true);
     else HDCM_GATE_LAUNCH(true, false);
@@ -935,8 +958,9 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
 // ------------------------------------------------------------------ plain attention pass
 extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, int64_t k_col,
                                     int64_t v_col, const void* gamma, int phi, void* ws, size_t ws_bytes,
-                                    void* out, int64_t out_row_stride, int64_t out_col, int64_t B, int64_t L,
-                                    int64_t dm, int64_t H, int64_t C, int dtype, void* stream) {
+                                    void* out, int64_t out_row_stride, int64_t out_col, const void* chain,
+                                    int64_t chain_row_stride, int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C,
+                                    int dtype, void* stream) {
   SlotPlan pl;
   int st = slot_plan(B, L, dm, H, C, dtype, &pl);
   if (st) return st;
@@ -952,6 +976,9 @@ extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_
                      dm % E == 0,
                  HDCM_EALIGN);
   HDCM_CHECK_ARG(((uintptr_t)out % 16) == 0 && out_col % 4 == 0 && aors % 4 == 0, HDCM_EALIGN);
+  const int64_t azrs = chain_row_stride < 0 ? -chain_row_stride : chain_row_stride;
+  HDCM_CHECK_ARG(!chain || (azrs >= out_col + dm && azrs < ((int64_t)1 << 31)), HDCM_EINVAL);
+  HDCM_CHECK_ARG(!chain || (((uintptr_t)chain % 8) == 0 && azrs % 4 == 0), HDCM_EALIGN);
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= slot_ws_bytes(B, H, pl), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
@@ -960,6 +987,11 @@ extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_
   if (pl.HD == HDV && (phi != 0) == PH) {                                                                    \
     st = launch_state<TT, HDV, PH>(base, row_stride, k_col, v_col - k_col, gamma, nullptr, ws, B, L, H, pl, s); \
     if (st) return st;                                                                                       \
+    if (chain)                                                                                               \
+      return launch_gate<TT, HDV, PH, false, true>(base, row_stride, q_col, k_col - q_col, v_col - q_col, 0,  \
+                                                   gamma, nullptr, nullptr, 0.f, ws, out, out_row_stride,    \
+                                                   out_col, nullptr, B, L, H, C, pl, s, chain,               \
+                                                   chain_row_stride);                                        \
     return launch_gate<TT, HDV, PH, false>(base, row_stride, q_col, k_col - q_col, v_col - q_col, 0, gamma,   \
                                            nullptr, nullptr, 0.f, ws, out, out_row_stride, out_col, nullptr, \
                                            B, L, H, C, pl, s);                                              \

@@ -154,12 +154,13 @@ class SlotSsmMixerFunction(torch.autograd.Function):
         dgw, dgb = _ops.gnorm_gate_bwd(y, projs[..., g_col:], gn_w, gn_b, 1e-5, dcomb[..., ds:], H,
                                        z[..., :dm], dprojs[..., g_col:])
         _ops.slot_phi_prep(projs, q_col, dm, z)
-        _ops.slot_attend(z, 0, dm, 2 * dm, gamma, dm, H, C, False, dprojs, q_col, ws=ws)  # d phi(q)
+        # d q = d phi(q) * phi'(q) and d k likewise: the passes multiply by phi' of the
+        # projections (chain) as they store
+        _ops.slot_attend(z, 0, dm, 2 * dm, gamma, dm, H, C, False, dprojs, q_col, ws=ws, chain=projs)  # d q
         _ops.slot_attend(z, 2 * dm, 3 * dm, 0, gamma, dm, H, C, False, dprojs, q_col + 2 * dm, reverse=True,
                          ws=ws)  # d v
         _ops.slot_attend(z, dm, 0, 3 * dm, gamma, dm, H, C, False, dprojs, q_col + dm, reverse=True,
-                         ws=ws)  # d phi(k)
-        _ops.slot_phi_chain(projs, q_col, dm, dprojs)
+                         ws=ws, chain=projs)  # d k
         dA = _ops.ssm_bwd(projs, A_log, ds, combined[..., :ds], dcomb[..., :ds], dprojs)
         return (dprojs, dA.to(A_log.dtype), None, dgw.to(gn_w.dtype), dgb.to(gn_b.dtype), None, None, None, None)
 

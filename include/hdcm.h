@@ -155,13 +155,18 @@ int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col
  * pair above (hdcm_slot_workspace_bytes).  The slot memory's backward runs it four times:
  * to recompute y (phi, forward) and for dphi(q) (identity: q=dy, k=v, v=phi(k)), dv
  * (backwards: q=phi(k), k=phi(q), v=dy) and dphi(k) (backwards: q=v, k=dy, v=phi(q)).
+ * With `chain` non-NULL each output value is multiplied by phi'(z) = 1 (z > 0) else exp(z),
+ * z read from `chain` at the output's own row and column (chain has out's column layout and
+ * row stride chain_row_stride, negative with a negative out_row_stride): dphi(q) and dphi(k)
+ * become dq and dk in the same pass.
  * No reference counterpart (the reference's slot kernel has no backward,
  * hdcmamba/model.py:236-272,340-384); the weights are those of model.py:265-272.
  */
 int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, int64_t k_col,
                          int64_t v_col, const void* gamma, int phi, void* ws, size_t ws_bytes,
-                         void* out, int64_t out_row_stride, int64_t out_col, int64_t B, int64_t L,
-                         int64_t dm, int64_t H, int64_t C, int dtype, void* stream);
+                         void* out, int64_t out_row_stride, int64_t out_col, const void* chain,
+                         int64_t chain_row_stride, int64_t B, int64_t L, int64_t dm, int64_t H,
+                         int64_t C, int dtype, void* stream);
 
 /*
  * Gradient of the per-token, per-head GroupNorm (eps, affine gn_w/gn_b over hd = dm/H

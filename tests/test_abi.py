@@ -249,20 +249,24 @@ def test_rowln_bwd_validation():
 def test_backward_entry_points_validation():
     lib = _ops.lib()
     # hdcm_slot_attend_fwd(base, rs, q_col, k_col, v_col, gamma, phi, ws, ws_bytes, out, ors, out_col,
-    #                      B, L, dm, H, C, dtype, stream)
+    #                      chain, chain_rs, B, L, dm, H, C, dtype, stream)
     f = lib.hdcm_slot_attend_fwd
     ws_n = lib.hdcm_slot_workspace_bytes(1, 128, 256, 4, 64, 1)
-    base = [P16, 1024, 256, 512, 0, P16, 0, P16, ws_n, P16, 256, 0, 1, 128, 256, 4, 64, 1, None]
+    base = [P16, 1024, 256, 512, 0, P16, 0, P16, ws_n, P16, 256, 0, None, 0, 1, 128, 256, 4, 64, 1, None]
     a = list(base); a[1] = 700  # row shorter than the v block at column 512 + 256
     assert f(*a) == EINVAL
     a = list(base); a[3] = 516  # block not on a 16-byte boundary
     assert f(*a) == EALIGN
-    a = list(base); a[1] = -1024; a[10] = -256; a[13] = 0  # negative strides accepted (empty: no launch)
+    a = list(base); a[1] = -1024; a[10] = -256; a[15] = 0  # negative strides accepted (empty: no launch)
     assert f(*a) == OK
     a = list(base); a[8] = ws_n - 1
     assert f(*a) == EWORKSPACE
-    a = list(base); a[14] = 240; a[15] = 5  # head dim 48
+    a = list(base); a[16] = 240; a[17] = 5  # head dim 48
     assert f(*a) == EUNSUPPORTED
+    a = list(base); a[12] = P16; a[13] = 200  # chain rows shorter than out's block
+    assert f(*a) == EINVAL
+    a = list(base); a[12] = P16; a[13] = 258  # chain rows not 8-byte aligned
+    assert f(*a) == EALIGN
     # hdcm_ssm_bwd(projs, prs, A_log, h, hrs, gy, gyrs, dprojs, drs, dA, ws, ws_bytes, B, L, ds, dtype, stream)
     g = lib.hdcm_ssm_bwd
     n = lib.hdcm_ssm_bwd_workspace_bytes(1, 100, 64, 1)

@@ -173,7 +173,8 @@ ATTEND_CASES = [
 @pytest.mark.parametrize("phi,reverse", [(True, False), (False, False), (False, True)])
 def test_slot_attend(dev, dtype, B, L, dm, H, C, phi, reverse):
     """The slot recurrence without GroupNorm/gate on three column blocks of one buffer in a
-    shuffled order (v, q, k, plus an unused block), forwards or backwards in time."""
+    shuffled order (v, q, k, plus an unused block), forwards or backwards in time; then with
+    the feature map's chain rule applied as the outputs are stored."""
     _say("slot_attend", dtype, B, L, dm, H, C, phi, reverse)
     g = torch.Generator().manual_seed(L + dm + C + phi + 2 * reverse)
     hd = dm // H
@@ -197,6 +198,16 @@ def test_slot_attend(dev, dtype, B, L, dm, H, C, phi, reverse):
     lim = 1e-4 if dtype == torch.float32 else 2e-2
     err = ((got - ref.reshape(B, L, dm)).abs().max() / ref.abs().max()).item()
     assert err <= lim, err
+    # chain: out *= phi'(z), z from a buffer with out's column layout (d phi -> d q / d k)
+    z = torch.randn(B, L, 8 + dm, generator=g).to(dtype)
+    zz = z[..., 8:].float()
+    ref_c = ref.reshape(B, L, dm) * torch.where(zz > 0, torch.ones_like(zz), torch.exp(zz))
+    out.zero_()
+    _ops.slot_attend(base.to(dev), q_col, k_col, v_col, gamma.to(dev), dm, H, C, phi, out, 8, reverse=reverse,
+                     chain=z.to(dev))
+    got = out[..., 8:].float().cpu()
+    err = ((got - ref_c).abs().max() / ref_c.abs().max()).item()
+    assert err <= lim, ("chain", err)
 
 
 def test_slot_segments_env(dev, monkeypatch):
