@@ -163,7 +163,16 @@ def _rows2d(t: torch.Tensor, name: str):
 
 # ----------------------------------------------------------------------------- timing hook
 class _Timer:
-    """Records torch.cuda events around named launches (used by bench.py)."""
+    """Records torch.cuda events around named launches (used by bench.py).
+
+    Each bracketed launch is preceded by a short GPU spin (torch.cuda._sleep) on the same
+    stream.  Without it the start event is processed as soon as the host submits it, and
+    when the host is slower than the GPU (eager forwards of short kernels) the time the
+    host then spends submitting the launch is counted as kernel time.  With the stream
+    busy the start event runs right before the kernel, so an interval is the kernel's own
+    duration plus the event's."""
+
+    lead_cycles = 100_000
 
     def __init__(self):
         self.active = set()
@@ -171,6 +180,7 @@ class _Timer:
 
     def begin(self, name):
         if name in self.active:
+            torch.cuda._sleep(self.lead_cycles)
             ev = torch.cuda.Event(enable_timing=True)
             ev.record()
             return ev
