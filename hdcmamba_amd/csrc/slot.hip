@@ -49,7 +49,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kTargetWorkgroups = 1024;
+// Segments are sized for about two workgroups per CU (512 on 256 CUs).  At B=1, L=32768,
+// 16 heads the measured forward prefers 16 tiles per segment (512 workgroups) to 8 (1024,
+// 1.3 rounds of the gate pass at 3 workgroups per CU) and to 4-13 or 22.
+constexpr int kTargetWorkgroups = 512;
 constexpr int kGateWavesPerEU = 3;  // register budget: 3 waves per SIMD (3 workgroups per CU)
 constexpr int kMinSegTiles = 4;
 
