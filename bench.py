@@ -5,8 +5,8 @@ Default workload: the 24-layer d_model=1024 (d_state 128, 16 heads, chunk 64, vo
 tied head) language model forward at B=1, L=32768 in bf16, uniform random token ids and
 random-init weights.  One step = one full forward (embedding, 24 blocks, final norms,
 logits), timed as replays of the forward recorded as a HIP graph.  Prints ONE JSON line
-with tokens/s, the roofline of the dominant custom kernel (HIP events on the launch stream
-around each custom kernel, over a second timed region of eager forwards), per-kernel
+with tokens/s, the roofline of the dominant custom kernel (HIP events recorded by each
+custom kernel's own dispatch, over a second timed region of eager forwards), per-kernel
 figures, and the CPU oracle's throughput on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2|lm_c5_decode|lm_c4_train]
@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA
 
 
 def _cpu_model():
@@ -63,17 +64,73 @@ def forward_totals(cfg, fused_out_proj=True):
     return n * blk_flops + tail_flops, n * blk_bytes + tail_bytes
 
 
-def kernel_bytes(cfg, name):
-    """Algorithmic HBM bytes per token of one launch of each custom kernel (bf16 eb=2)."""
+# Calls whose kernels bench.py times (hdcmamba_amd._ops wrapper names).
+KERNELS = ("norm_conv", "ssm", "slot_state", "slot_gate", "rowln", "rowln_gemm")
+
+
+def _mean(xs):
+    return sum(xs) / len(xs)
+
+
+def kernel_table(cfg, tokens, times):
+    """Per-kernel durations (microseconds, mean over launches) and roofline fractions from
+    the dispatch-timed calls `times` ({call: [[ms of each kernel of the call] per call]}).
+
+    Algorithmic HBM bytes per token (eb = element bytes): norm_conv 2 dm eb (read x, write
+    x_conv); SSM 4 ds eb (read dt, x, b; write y); slot_state 2 dm eb (read k, v); slot_gate
+    5 dm eb (read q, k, v, gate; write the gated output) -- also the bytes of the slot
+    operator as a whole (state pre-pass + segment scan + gate pass); rowln 2 dm eb.
+    out_proj (rowln_gemm) is MFMA-bound: 2 T (ds + dm) dm FLOPs against the bf16 peak."""
     eb = 2 if cfg["dtype_name"] == "bf16" else 4
     dm, ds = cfg["d_model"], cfg["d_state"]
-    return {
-        "norm_conv": 2 * dm * eb,          # read x, write x_conv
-        "ssm": 4 * ds * eb,                # read dt, x, b; write y
-        "slot_state": 2 * dm * eb,         # read k, v (pre-pass)
-        "slot_gate": 5 * dm * eb,          # read q, k, v, gate; write gated output
-        "rowln": 2 * (ds + dm) * eb,       # read + write combined row
-    }[name]
+
+    def hbm(us, nbytes, launches, **extra):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 2), "launches": launches, "bytes_per_launch": nbytes, "bound": "hbm",
+                "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), **extra}
+
+    out = {}
+    if "norm_conv" in times:
+        c = times["norm_conv"]
+        out["norm_conv"] = hbm(_mean([k[0] for k in c]) * 1e3, 2 * dm * eb * tokens, len(c))
+    if "ssm" in times:
+        c = times["ssm"]
+        per = [round(_mean([k[i] for k in c]) * 1e3, 2) for i in range(len(c[0]))]
+        out["ssm"] = hbm(sum(per), 4 * ds * eb * tokens, len(c), kernels_us=per,
+                         note="sum of the SSM's kernels")
+    if "slot_state" in times:
+        c = [k for k in times["slot_state"] if len(k) == 2]  # pre-pass + scan (more than one segment)
+        if c:
+            out["slot_state"] = hbm(_mean([k[0] for k in c]) * 1e3, 2 * dm * eb * tokens, len(c))
+            out["slot_scan"] = {"us": round(_mean([k[1] for k in c]) * 1e3, 2), "launches": len(c)}
+    if "slot_gate" in times:
+        c = times["slot_gate"]
+        out["slot_gate"] = hbm(_mean([k[0] for k in c]) * 1e3, 5 * dm * eb * tokens, len(c))
+    if "slot_gate" in out and "slot_state" in out:
+        us = out["slot_state"]["us"] + out["slot_scan"]["us"] + out["slot_gate"]["us"]
+        out["slot_op"] = hbm(us, 5 * dm * eb * tokens, out["slot_gate"]["launches"],
+                             note="slot_state + slot_scan + slot_gate against the gate pass's bytes")
+    if "rowln" in times:
+        c = times["rowln"]
+        out["rowln"] = hbm(_mean([k[0] for k in c]) * 1e3, 2 * dm * eb * tokens, len(c))
+    if "rowln_gemm" in times:
+        c = times["rowln_gemm"]
+        us = _mean([k[0] for k in c]) * 1e3
+        fl = 2 * tokens * (ds + dm) * dm
+        tfs = fl / (us * 1e-6) / 1e12
+        out["out_proj"] = {"us": round(us, 2), "launches": len(c), "flops_per_launch": fl, "bound": "mfma",
+                           "TFLOP/s": round(tfs, 1), "frac": round(tfs / MFMA_PEAK_TFS, 4),
+                           "note": "rowln_gemm: out_proj with the folded row LayerNorm and the residual"}
+    return out
+
+
+def roofline_of(k, traffic):
+    """The bench line's roofline object for one kernel_table entry."""
+    if k["bound"] == "mfma":
+        return {"bound": "mfma", "achieved": k["TFLOP/s"], "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": k["frac"], "traffic": traffic, "us": k["us"], "flops_per_launch": k["flops_per_launch"]}
+    return {"bound": "hbm", "achieved": k["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": k["frac"],
+            "traffic": traffic, "us": k["us"], "bytes_per_launch": k["bytes_per_launch"]}
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "slot_gate_lm_c4_traffic.md")
@@ -119,7 +176,7 @@ def pmc_summary(fetch_csv, write_csv, copy_bytes):
     gate = [k for k in out if k.startswith("slot_gate_kernel")]
     head = [f"copy calibration ({copy_bytes} bytes): FETCH_SIZE x {ff:.4f}, WRITE_SIZE x {fw:.4f}", ""]
     if gate:
-        head += [f"{TRAFFIC_KEY} {round(out[gate[0]])}", ""]
+        head += [f"{TRAFFIC_KEY} {round(out[gate[0]])}", f"{SOURCE_KEY} {slot_source_hash()}", ""]
     return "\n".join(head + lines) + "\n"
 
 
@@ -136,15 +193,33 @@ def stats_summary(stats_csv):
     return "\n".join(lines) + "\n"
 
 
+SOURCE_KEY = "slot_sources_sha256:"
+
+
+def slot_source_hash():
+    """sha256 over the sources that define slot_gate's kernels and launch plan."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in ("hdcmamba_amd/csrc/slot.hip", "hdcmamba_amd/csrc/hdcm_common.h"):
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def stored_traffic(workload):
-    """HBM bytes per slot_gate launch recorded by the counter runs for the L=32768 LM."""
+    """HBM bytes per slot_gate launch recorded by the counter runs for the L=32768 LM, or None
+    when the summary was made from other slot sources than the ones in this tree."""
     if workload != "lm_c4" or not os.path.exists(TRAFFIC_SUMMARY):
         return None
+    traffic, src = None, None
     with open(TRAFFIC_SUMMARY) as f:
         for line in f:
             if line.startswith(TRAFFIC_KEY):
-                return int(line.split(":", 1)[1])
-    return None
+                traffic = int(line.split(":", 1)[1])
+            elif line.startswith(SOURCE_KEY):
+                src = line.split(":", 1)[1].strip()
+    return traffic if src == slot_source_hash() else None
 
 
 def cpu_baseline(model, ids_gpu, cfg, budget_s):
@@ -154,8 +229,7 @@ def cpu_baseline(model, ids_gpu, cfg, budget_s):
 
     import oracle
 
-    threads = len(os.sched_getaffinity(0))
-    threads = min(threads, int(os.environ.get("HDCM_CPU_THREADS", "16")))
+    threads = len(os.sched_getaffinity(0))  # every core this process may run on
     torch.set_num_threads(threads)
     sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
     L = cfg["L"]
@@ -369,72 +443,33 @@ def main():
             runner(inp)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        # Per-kernel durations: HIP events on the launch stream around every custom kernel,
-        # over eager forwards (launches inside a graph replay cannot be bracketed).
+        # Per-kernel durations: every custom kernel of k_steps eager forwards records a pair of
+        # HIP events from its own dispatch timestamps (hdcm_time_launches; launches inside a
+        # graph replay cannot carry events).  The events add nothing to the stream, so these
+        # forwards also give the eager rate.
         k_steps = max(1, min(args.steps, 5))
         model(inp)
         torch.cuda.synchronize()
+        _ops.timer.active = set(KERNELS)
         t2 = time.perf_counter()
         for _ in range(k_steps):
             model(inp)
         torch.cuda.synchronize()
         t3 = time.perf_counter()
-        # the timed launches are preceded by a GPU spin each (see _ops._Timer), so these
-        # forwards are not the eager rate above
-        _ops.timer.active = {"norm_conv", "ssm", "slot_state", "slot_gate", "rowln", "rowln_gemm"}
-        for _ in range(k_steps):
-            model(inp)
-        torch.cuda.synchronize()
         _ops.timer.active = set()
-        # the same bracket with no launch inside: what the events add to every interval
-        bracket = []
-        for _ in range(32):
-            torch.cuda._sleep(_ops.timer.lead_cycles)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            e1.record()
-            bracket.append((e0, e1))
-        torch.cuda.synchronize()
-        bracket_us = sorted(a.elapsed_time(b) for a, b in bracket)[len(bracket) // 2] * 1e3
     times = _ops.timer.collect()
     sec = t1 - t0
     ms_per_step = sec / args.steps * 1e3
     value = tokens * args.steps / sec
     eager_ms = (t3 - t2) / k_steps * 1e3
-
-    kernels = {}
-    for name, ms in times.items():
-        # launch duration = event interval minus the empty bracket measured the same way
-        us_raw = sum(ms) / len(ms) * 1e3
-        us = us_raw - bracket_us
-        if name == "rowln_gemm":  # MFMA-bound: out_proj's FLOPs
-            tfs = 2 * tokens * (cfg["d_state"] + cfg["d_model"]) * cfg["d_model"] / (us * 1e-6) / 1e12
-            kernels[name] = {"us": round(us, 2), "us_raw": round(us_raw, 2), "launches": len(ms),
-                             "TFLOP/s": round(tfs, 1), "frac_bf16_mfma": round(tfs / 2500.0, 4)}
-            continue
-        gbs = kernel_bytes(cfg, name) * tokens / (us * 1e-6) / 1e9
-        kernels[name] = {"us": round(us, 2), "us_raw": round(us_raw, 2), "launches": len(ms),
-                         "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-    dom = "slot_gate"
-    d = kernels[dom]
-    roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": d["frac_hbm"], "traffic": stored_traffic(args.workload),
-                "bytes_per_launch": kernel_bytes(cfg, dom) * tokens}
+    kernels = kernel_table(cfg, tokens, times)
+    roofline = roofline_of(kernels["slot_gate"], stored_traffic(args.workload))
+    # the slot operator as a whole (state pre-pass, segment scan, gate pass) against the
+    # gate pass's algorithmic bytes (q, k, v, gate read once, output written once)
+    roofline_slot_op = roofline_of(kernels["slot_op"], None) if "slot_op" in kernels else None
     # the fused out_proj (LayerNorm folded into the GEMM) is the largest kernel of this build by
     # time; it is MFMA-bound, so its roofline is FLOPs against the bf16 dense peak
-    roofline_out_proj = None
-    if "rowln_gemm" in kernels:
-        k = kernels["rowln_gemm"]
-        fl = 2 * tokens * (cfg["d_state"] + cfg["d_model"]) * cfg["d_model"]
-        roofline_out_proj = {"kernel": "rowln_gemm (out_proj with the folded LayerNorm and the residual)",
-                             "bound": "mfma", "achieved": k["TFLOP/s"], "peak": 2500.0, "unit": "TFLOP/s",
-                             "frac": k["frac_bf16_mfma"], "traffic": None, "flops_per_launch": fl}
-    if "slot_state" in kernels:
-        us = kernels["slot_state"]["us"] + kernels["slot_gate"]["us"]
-        gbs = kernel_bytes(cfg, "slot_gate") * tokens / (us * 1e-6) / 1e9
-        kernels["slot_op(state+gate)"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
-                                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    roofline_out_proj = roofline_of(kernels["out_proj"], None) if "out_proj" in kernels else None
 
     forward_summary = None
     if args.workload.startswith("lm"):
@@ -460,17 +495,18 @@ def main():
                    "vocab": 50304 if args.workload.startswith("lm") else None,
                    "global_batch": cfg["B"], "seq_len": cfg["L"], "parallelism": "none (1 GPU)",
                    "fused_out_proj": args.fused_out_proj == "on"},
-        "roofline": roofline,
-        "roofline_out_proj": roofline_out_proj,
+        "roofline": dict(kernel="slot_gate (slot memory + GroupNorm + gate pass)", **roofline),
+        "roofline_slot_op": (dict(kernel="slot operator: slot_state + slot_scan + slot_gate", **roofline_slot_op)
+                             if roofline_slot_op else None),
+        "roofline_out_proj": (dict(kernel="rowln_gemm: out_proj with the folded LayerNorm and the residual",
+                                   **roofline_out_proj) if roofline_out_proj else None),
         "cpu_baseline": cpu,
         "kernels": kernels,
         "forward": forward_summary,
         "timing": {"steps": "HIP graph replays of the whole forward" if use_graph else "eager forwards",
-                   "kernels": f"HIP events around each custom kernel over {k_steps} eager forwards",
-                   "eager_ms_per_step": round(eager_ms, 3),
-                   "empty_bracket_us": round(bracket_us, 2),
-                   "note": "kernel us = event interval (us_raw) minus empty_bracket_us, the "
-                           "interval of the same event pair around no launch"},
+                   "kernels": (f"HIP events recorded by each custom kernel's own dispatch (begin and end "
+                               f"timestamps, hipExtLaunchKernel) over {k_steps} eager forwards; mean per launch"),
+                   "eager_ms_per_step": round(eager_ms, 3)},
         "gemm_solutions": (f"TunableOp file, {n_tuned} recorded GEMM signatures" if n_tuned
                            else "library default heuristics"),
         "gpu": torch.cuda.get_device_name(0),

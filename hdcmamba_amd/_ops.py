@@ -23,6 +23,8 @@ _DTYPES = {torch.float32: HDCM_F32, torch.bfloat16: HDCM_BF16}
 _PROTOS = {
     "hdcm_abi_version": (c_int, []),
     "hdcm_strerror": (ctypes.c_char_p, [c_int]),
+    "hdcm_time_launches": (c_int, [c_void_p, c_void_p, c_int]),
+    "hdcm_timed_launch_count": (c_int, []),
     "hdcm_norm_conv_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_float,
                                    c_int, c_void_p]),
@@ -162,39 +164,93 @@ def _rows2d(t: torch.Tensor, name: str):
 
 
 # ----------------------------------------------------------------------------- timing hook
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime this process already uses (torch's copy, which libhdcmamba_hip.so
+    binds to through the shared soname), with the event calls declared."""
+    path = "libamdhip64.so.7"
+    try:
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64" in line:
+                    path = line.split()[-1]
+                    break
+    except OSError:
+        pass
+    h = ctypes.CDLL(path)
+    h.hipEventCreate.restype = c_int
+    h.hipEventCreate.argtypes = [ctypes.POINTER(c_void_p)]
+    h.hipEventDestroy.restype = c_int
+    h.hipEventDestroy.argtypes = [c_void_p]
+    h.hipEventSynchronize.restype = c_int
+    h.hipEventSynchronize.argtypes = [c_void_p]
+    h.hipEventElapsedTime.restype = c_int
+    h.hipEventElapsedTime.argtypes = [ctypes.POINTER(c_float), c_void_p, c_void_p]
+    return h
+
+
 class _Timer:
-    """Records torch.cuda events around named launches (used by bench.py).
+    """Kernel durations of named calls (used by bench.py).
 
-    Each bracketed launch is preceded by a short GPU spin (torch.cuda._sleep) on the same
-    stream.  Without it the start event is processed as soon as the host submits it, and
-    when the host is slower than the GPU (eager forwards of short kernels) the time the
-    host then spends submitting the launch is counted as kernel time.  With the stream
-    busy the start event runs right before the kernel, so an interval is the kernel's own
-    duration plus the event's."""
+    For a call whose name is in ``active``, hdcm_time_launches arms event pairs for the
+    call's kernels: the k-th kernel it launches records pair k from its own dispatch
+    timestamps (begin, end), so no event packets enter the stream and each interval is
+    exactly one kernel's execution."""
 
-    lead_cycles = 100_000
+    max_launches = 8  # kernels per call that get events
 
     def __init__(self):
         self.active = set()
         self.events = {}
+        self._rt = None
+        self._armed = None
+
+    def _event(self):
+        if self._rt is None:
+            self._rt = _hip_runtime()
+        ev = c_void_p()
+        if self._rt.hipEventCreate(ctypes.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev.value
 
     def begin(self, name):
-        if name in self.active:
-            torch.cuda._sleep(self.lead_cycles)
-            ev = torch.cuda.Event(enable_timing=True)
-            ev.record()
-            return ev
-        return None
+        if name not in self.active:
+            return None
+        n = self.max_launches
+        starts = (c_void_p * n)(*[self._event() for _ in range(n)])
+        stops = (c_void_p * n)(*[self._event() for _ in range(n)])
+        _check("hdcm_time_launches", lib().hdcm_time_launches(starts, stops, n))
+        return starts, stops
 
-    def end(self, name, ev0):
-        if ev0 is not None:
-            ev1 = torch.cuda.Event(enable_timing=True)
-            ev1.record()
-            self.events.setdefault(name, []).append((ev0, ev1))
+    def end(self, name, arrays):
+        if arrays is None:
+            return
+        used = lib().hdcm_timed_launch_count()
+        _check("hdcm_time_launches", lib().hdcm_time_launches(None, None, 0))
+        starts, stops = arrays
+        for k in range(used, self.max_launches):  # pairs no kernel recorded
+            self._rt.hipEventDestroy(starts[k])
+            self._rt.hipEventDestroy(stops[k])
+        self.events.setdefault(name, []).append([(starts[k], stops[k]) for k in range(used)])
+
+    def _elapsed(self, a, b):
+        t = c_float()
+        rc = self._rt.hipEventSynchronize(b) or self._rt.hipEventElapsedTime(ctypes.byref(t), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return t.value
 
     def collect(self):
+        """{name: [[ms of kernel k of the call for k in its launches] per timed call]};
+        releases the events."""
         torch.cuda.synchronize()
-        out = {k: [a.elapsed_time(b) for a, b in v] for k, v in self.events.items()}
+        out = {}
+        for name, calls in self.events.items():
+            out[name] = []
+            for pairs in calls:
+                out[name].append([self._elapsed(a, b) for a, b in pairs])
+                for a, b in pairs:
+                    self._rt.hipEventDestroy(a)
+                    self._rt.hipEventDestroy(b)
         self.events = {}
         return out
 

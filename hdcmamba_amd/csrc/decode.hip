@@ -270,7 +270,7 @@ int launch_norm_conv_step(const void* x, int64_t x_rs, const void* ln_w, const v
   const int ng = (int)((G + kThreads - 1) / kThreads);
 #define HDCM_NCS_CASE(N)                                                                             \
   if (ng == N) {                                                                                     \
-    hipLaunchKernelGGL((norm_conv_step_kernel<T, N>), dim3((unsigned)B), dim3(kThreads), 0, s,      \
+    HDCM_LAUNCH((norm_conv_step_kernel<T, N>), dim3((unsigned)B), dim3(kThreads), 0, s,      \
                        (const T*)x, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,          \
                        (const T*)conv_b, (T*)hist, (T*)out, o_rs, (int)D, eps);                      \
     return hdcm_launch_status();                                                                     \
@@ -333,7 +333,7 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
   const dim3 grid((unsigned)(H + 1), (unsigned)B);
 #define HDCM_MIX_CASE(TT, HDV)                                                                              \
   if (hd == HDV) {                                                                                           \
-    hipLaunchKernelGGL((mixer_step_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)projs,          \
+    HDCM_LAUNCH((mixer_step_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)projs,          \
                        proj_row_stride, (int)q_col, (int)dm, (const TT*)gamma, S_prev, S_intra, (int)pos,    \
                        (const int*)pos_dev, (int)C, (const TT*)gn_w, (const TT*)gn_b, gn_eps,               \
                        (const TT*)A_log, h, (int)ds, (TT*)out, out_row_stride, (int)y_col, (int)g_col);      \
@@ -356,7 +356,7 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
 
 extern "C" int hdcm_chunk_pos_advance(int32_t* pos_dev, int64_t C, void* stream) {
   HDCM_CHECK_ARG(pos_dev != nullptr && C > 0 && C < ((int64_t)1 << 24), HDCM_EINVAL);
-  hipLaunchKernelGGL(chunk_pos_advance_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, (int*)pos_dev,
+  HDCM_LAUNCH(chunk_pos_advance_kernel, dim3(1), dim3(kWave), 0, (hipStream_t)stream, (int*)pos_dev,
                      (int)C);
   return hdcm_launch_status();
 }

@@ -309,7 +309,7 @@ extern "C" int hdcm_gemm_fwd(const void* x, int64_t x_row_stride, const void* w,
   if (M == 0) return HDCM_OK;
   const int64_t n_ot = (N + kBO - 1) / kBO, n_tt = (M + kBT - 1) / kBT;
   auto kern = bias ? gemm_bt_kernel<EPI_BIAS, true> : gemm_bt_kernel<EPI_BIAS, false>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)x,
+  HDCM_LAUNCH(kern, dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)x,
                      x_row_stride, (const bf16_t*)w, w_row_stride, (const bf16_t*)bias, (const bf16_t*)nullptr,
                      (int64_t)0, (bf16_t*)out, out_row_stride, (int)M, (int)N, (int)K, (int)n_ot, 0.f);
   return hdcm_launch_status();
@@ -329,7 +329,7 @@ extern "C" int hdcm_rowln_gemm_fwd(const void* c, int64_t c_row_stride, const vo
     return hdcm_skinny_rowln(c, c_row_stride, w, w_row_stride, res, res_row_stride, out, out_row_stride, M, N, K,
                              eps, (hipStream_t)stream);
   const int64_t n_ot = (N + kBO - 1) / kBO, n_tt = (M + kBT - 1) / kBT;
-  hipLaunchKernelGGL((gemm_bt_kernel<EPI_ROWLN, false>), dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0,
+  HDCM_LAUNCH((gemm_bt_kernel<EPI_ROWLN, false>), dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const bf16_t*)c, c_row_stride, (const bf16_t*)w, w_row_stride,
                      (const bf16_t*)nullptr, (const bf16_t*)res, res_row_stride, (bf16_t*)out, out_row_stride, (int)M,
                      (int)N, (int)K, (int)n_ot, eps);

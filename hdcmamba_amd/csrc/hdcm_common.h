@@ -5,10 +5,35 @@
 // round-to-nearest-even, the rounding torch and the MFMA operand path use.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/hdcm.h"
+
+// ------------------------------------------------------------ launch timing hook
+// hdcm_time_launches(starts, stops, n) (api.hip) arms the calling thread: the k-th kernel it
+// launches through HDCM_LAUNCH (k < n) records starts[k] when it begins and stops[k] when it
+// ends, from the dispatch's own timestamps (hipExtLaunchKernel).  Launches past n, and all
+// launches of an unarmed thread, are plain hipLaunchKernelGGL.
+struct HdcmTiming {
+  void* const* start;
+  void* const* stop;
+  int n, used;
+};
+extern thread_local HdcmTiming hdcm_timing_slot;
+
+#define HDCM_LAUNCH(kernel, grid, block, shmem, stream, ...)                                      \
+  do {                                                                                            \
+    if (hdcm_timing_slot.used < hdcm_timing_slot.n) {                                             \
+      const int k_ = hdcm_timing_slot.used++;                                                     \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream,                                   \
+                            (hipEvent_t)hdcm_timing_slot.start[k_],                               \
+                            (hipEvent_t)hdcm_timing_slot.stop[k_], 0u, __VA_ARGS__);              \
+    } else {                                                                                      \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                        \
+    }                                                                                             \
+  } while (0)
 
 namespace hdcm {
 
@@ -308,7 +333,7 @@ static inline int hdcm_launch_status() {
 // Launch colsum_kernel (see there) on `s`; nk == 0 writes zeros.
 static inline int hdcm_colsum(const float* part, int64_t kstride, int nk, int ncols, int cgroup, int64_t gstride,
                               float* out0, int nsplit, float* out1, hipStream_t s) {
-  hipLaunchKernelGGL(hdcm::colsum_kernel, dim3((unsigned)((ncols + hdcm::kSumCols - 1) / hdcm::kSumCols)),
+  HDCM_LAUNCH(hdcm::colsum_kernel,dim3((unsigned)((ncols + hdcm::kSumCols - 1) / hdcm::kSumCols)),
                      dim3(hdcm::kSumCols * hdcm::kSumRows), 0, s, part, kstride, nk, ncols, cgroup, gstride, out0,
                      nsplit, out1);
   return hdcm_launch_status();

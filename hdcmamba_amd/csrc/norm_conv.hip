@@ -177,7 +177,7 @@ void launch_rows(const void* x, int64_t x_bs, int64_t x_rs, const void* ln_w, co
                  int64_t B, int64_t L, int64_t D, float eps, hipStream_t s) {
   const int64_t rows_per_block = (int64_t)kWavesPerBlock * kRows;
   dim3 grid((unsigned)((L + rows_per_block - 1) / rows_per_block), (unsigned)B);
-  hipLaunchKernelGGL((norm_conv_kernel<T, NG, kRows>), grid, dim3(kWavesPerBlock * kWave), 0, s,
+  HDCM_LAUNCH((norm_conv_kernel<T, NG, kRows>), grid, dim3(kWavesPerBlock * kWave), 0, s,
                      (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,
                      (const T*)conv_b, (T*)out, o_bs, o_rs, (int)L, (int)D, eps);
 }

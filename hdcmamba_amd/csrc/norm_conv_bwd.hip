@@ -321,7 +321,7 @@ int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_
   const dim3 rgrid((unsigned)((L + kRowsWPB * kRunRows - 1) / (kRowsWPB * kRunRows)), (unsigned)B);
 #define HDCM_BWD_ROWS(N)                                                                                         \
   if (ng == N)                                                                                                   \
-    hipLaunchKernelGGL((norm_conv_bwd_rows_kernel<T, N>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
+    HDCM_LAUNCH((norm_conv_bwd_rows_kernel<T, N>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
                        g_bs, g_rs, (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)conv_w, (T*)dx, d_bs, d_rs, \
                        stats, (int)L, (int)D, eps);
   HDCM_BWD_ROWS(1)
@@ -330,7 +330,7 @@ int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_
   int st = hdcm_launch_status();
   if (st) return st;
   const dim3 cgrid((unsigned)((G + kColThreads - 1) / kColThreads), (unsigned)nchunk, (unsigned)B);
-  hipLaunchKernelGGL((norm_conv_bwd_cols_kernel<T>), cgrid, dim3(kColThreads), 0, s, (const T*)go, g_bs, g_rs,
+  HDCM_LAUNCH((norm_conv_bwd_cols_kernel<T>), cgrid, dim3(kColThreads), 0, s, (const T*)go, g_bs, g_rs,
                      (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)ln_b, (const T*)conv_w,
                      (const float2*)stats, part, (int)L, (int)D, (int)nchunk);
   st = hdcm_launch_status();

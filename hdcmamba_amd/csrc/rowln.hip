@@ -94,11 +94,11 @@ void launch_shape(const void* in, int64_t in_rs, void* out, int64_t out_rs, cons
   const int64_t per_block = (int64_t)WPB * R;
   dim3 grid((unsigned)((rows + per_block - 1) / per_block));
   if (w)
-    hipLaunchKernelGGL((rowln_kernel<T, NG, true, R, WPB>), grid, dim3(WPB * kWave), 0, s,
+    HDCM_LAUNCH((rowln_kernel<T, NG, true, R, WPB>), grid, dim3(WPB * kWave), 0, s,
                        (const T*)in, in_rs, (T*)out, out_rs, (const T*)w, (const T*)b, rows, (int)W,
                        eps);
   else
-    hipLaunchKernelGGL((rowln_kernel<T, NG, false, R, WPB>), grid, dim3(WPB * kWave), 0, s,
+    HDCM_LAUNCH((rowln_kernel<T, NG, false, R, WPB>), grid, dim3(WPB * kWave), 0, s,
                        (const T*)in, in_rs, (T*)out, out_rs, (const T*)nullptr,
                        (const T*)nullptr, rows, (int)W, eps);
 }
@@ -294,13 +294,13 @@ int launch_bwd_ng(const void* dy, int64_t dy_rs, const void* x, int64_t x_rs, co
                   int64_t dx_rs, float* dw, float* db, float* ws, int64_t rows, int W, float eps, hipStream_t s) {
   const int64_t nb = bwd_blocks(rows);
   if (w) {
-    hipLaunchKernelGGL((rowln_bwd_rows_kernel<T, NG, true>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
+    HDCM_LAUNCH((rowln_bwd_rows_kernel<T, NG, true>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
                        (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)w, (T*)dx, dx_rs, ws, rows, W, eps);
     int st = hdcm_launch_status();
     if (st) return st;
     return hdcm_colsum(ws, 2 * (int64_t)W, (int)nb, 2 * W, 2 * W, 0, dw, W, db, s);
   } else {
-    hipLaunchKernelGGL((rowln_bwd_rows_kernel<T, NG, false>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
+    HDCM_LAUNCH((rowln_bwd_rows_kernel<T, NG, false>), dim3((unsigned)nb), dim3(kBwdWaves * kWave), 0, s,
                        (const T*)dy, dy_rs, (const T*)x, x_rs, (const T*)nullptr, (T*)dx, dx_rs, ws, rows, W, eps);
   }
   return hdcm_launch_status();

@@ -232,17 +232,17 @@ void launch_lds(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const 
   const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
   bf16_t* o = (bf16_t*)out;
   if (bias && res)
-    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, true, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (bias)
-    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, true, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (res)
-    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else
-    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
-                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
+                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
 }
 
 template <int STEPS>
@@ -252,17 +252,17 @@ void launch_steps(const void* A, int64_t a_rs, const void* W, int64_t w_rs, cons
   const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
   bf16_t* o = (bf16_t*)out;
   if (bias && res)
-    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, true, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs, bs,
-                       rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_gemm_kernel<STEPS, true, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs, bs,
+                       rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (bias)
-    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, true, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_gemm_kernel<STEPS, true, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (res)
-    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_gemm_kernel<STEPS, false, true>), grid, dim3(kThreads), 0, s, a, a_rs, wt, w_rs,
+                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt,
-                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K);
+    HDCM_LAUNCH((skinny_gemm_kernel<STEPS, false, false>), grid, dim3(kThreads), 0, s, a, a_rs, wt,
+                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
 }
 
 template <int STEPS, bool WIDE>
@@ -270,10 +270,10 @@ void launch_ln(const bf16_t* c, int64_t c_rs, const bf16_t* W, int64_t w_rs, con
                bf16_t* out, int64_t o_rs, int M, int N, int K, float eps, hipStream_t s) {
   const dim3 grid((unsigned)((N + 15) / 16));
   if constexpr (WIDE)
-    hipLaunchKernelGGL((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
                        w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
   else
-    hipLaunchKernelGGL((skinny_gemm_kernel<STEPS, false, true, true>), grid, dim3(kThreads), 0, s, c, c_rs, W,
+    HDCM_LAUNCH((skinny_gemm_kernel<STEPS, false, true, true>), grid, dim3(kThreads), 0, s, c, c_rs, W,
                        w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
 }
 

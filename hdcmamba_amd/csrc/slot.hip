@@ -388,7 +388,16 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     const int tl = min(TC, L - pt);
     const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * grs + gcol;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) graw[g] = *reinterpret_cast<const uint4*>(grow + g * gstep);
+    for (int g = 0; g < NG; ++g) {
+      if constexpr (kPairs || sizeof(T) == 4) {
+        graw[g] = *reinterpret_cast<const uint4*>(grow + g * gstep);
+      } else {
+        // bf16 without 16-byte runs: the 4 values used (8 bytes), so the last head's read
+        // ends at its own last column
+        const uint2 v = *reinterpret_cast<const uint2*>(grow + g * gstep);
+        graw[g] = make_uint4(v.x, v.y, 0u, 0u);
+      }
+    }
   };
   if ((EPI || CHAIN) && w < NIT) load_gate(p_begin);
 
@@ -781,7 +790,7 @@ int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype,
   if (dtype != HDCM_F32 && dtype != HDCM_BF16) return HDCM_EUNSUPPORTED;
   if (B < 0 || L < 0 || dm <= 0 || H <= 0 || C <= 0 || dm % H) return HDCM_EINVAL;
   const int64_t HD = dm / H;
-  if (HD != 32 && HD != 64 && HD != 96) return HDCM_EUNSUPPORTED;
+  if (HD != 32 && HD != 64 && HD != 96 && HD != 128) return HDCM_EUNSUPPORTED;
   const int TC = dtype == HDCM_BF16 ? 64 : 32;
   if (L % C) return HDCM_EINVAL;
   int cshift = 31;
@@ -830,13 +839,13 @@ int launch_state(const void* base, int64_t prs, int64_t k_col, int64_t v_off, co
   float* U = (float*)ws;
   float* Ain = U + (size_t)B * H * pl.nseg * HD * HD;
   if (pl.nseg > 1) {
-    hipLaunchKernelGGL((slot_state_kernel<T, HD, TC, PHI>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
+    HDCM_LAUNCH((slot_state_kernel<T, HD, TC, PHI>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
                        dim3(kThreads), 0, s, (const T*)base, prs, (int)k_col, (int)v_off, (int)L,
                        (const T*)gamma, pl.seg_tiles, pl.nseg, U);
     const int st = hdcm_launch_status();
     if (st) return st;
   }
-  hipLaunchKernelGGL((slot_scan_kernel<T>), dim3((HD * HD + kThreads - 1) / kThreads, (unsigned)H, (unsigned)B),
+  HDCM_LAUNCH((slot_scan_kernel<T>), dim3((HD * HD + kThreads - 1) / kThreads, (unsigned)H, (unsigned)B),
                      dim3(kThreads), 0, s, U, S0, Ain, (const T*)gamma, HD * HD, pl.nseg,
                      pl.seg_tiles * TC);
   return hdcm_launch_status();
@@ -857,7 +866,7 @@ int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int
   const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0 &&
                      (!CHAIN || (((uintptr_t)zb % 16) == 0 && zrs % 8 == 0));
 #define HDCM_GATE_LAUNCH(W, P)                                                                              \
-  hipLaunchKernelGGL((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
+  HDCM_LAUNCH((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
                      (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
                      pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, \
                      pl.nseg, (T*)out, ors, (int)out_col, S_final, (const T*)zb, zrs)
@@ -910,10 +919,12 @@ extern "C" int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, i
     HDCM_STATE_CASE(bf16_t, 32)
     HDCM_STATE_CASE(bf16_t, 64)
     HDCM_STATE_CASE(bf16_t, 96)
+    HDCM_STATE_CASE(bf16_t, 128)
   } else {
     HDCM_STATE_CASE(float, 32)
     HDCM_STATE_CASE(float, 64)
     HDCM_STATE_CASE(float, 96)
+    HDCM_STATE_CASE(float, 128)
   }
 #undef HDCM_STATE_CASE
   return HDCM_EUNSUPPORTED;
@@ -949,10 +960,12 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
     HDCM_GATE_CASE(bf16_t, 32)
     HDCM_GATE_CASE(bf16_t, 64)
     HDCM_GATE_CASE(bf16_t, 96)
+    HDCM_GATE_CASE(bf16_t, 128)
   } else {
     HDCM_GATE_CASE(float, 32)
     HDCM_GATE_CASE(float, 64)
     HDCM_GATE_CASE(float, 96)
+    HDCM_GATE_CASE(float, 128)
   }
 #undef HDCM_GATE_CASE
   return HDCM_EUNSUPPORTED;
@@ -1003,16 +1016,20 @@ extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_
     HDCM_ATTEND_CASE(bf16_t, 32, true)
     HDCM_ATTEND_CASE(bf16_t, 64, true)
     HDCM_ATTEND_CASE(bf16_t, 96, true)
+    HDCM_ATTEND_CASE(bf16_t, 128, true)
     HDCM_ATTEND_CASE(bf16_t, 32, false)
     HDCM_ATTEND_CASE(bf16_t, 64, false)
     HDCM_ATTEND_CASE(bf16_t, 96, false)
+    HDCM_ATTEND_CASE(bf16_t, 128, false)
   } else {
     HDCM_ATTEND_CASE(float, 32, true)
     HDCM_ATTEND_CASE(float, 64, true)
     HDCM_ATTEND_CASE(float, 96, true)
+    HDCM_ATTEND_CASE(float, 128, true)
     HDCM_ATTEND_CASE(float, 32, false)
     HDCM_ATTEND_CASE(float, 64, false)
     HDCM_ATTEND_CASE(float, 96, false)
+    HDCM_ATTEND_CASE(float, 128, false)
   }
 #undef HDCM_ATTEND_CASE
   return HDCM_EUNSUPPORTED;

@@ -320,7 +320,7 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
       const dim3 grid((unsigned)(nblk * nstripe));
 #define HDCM_GNS_CASE(TT, HDV)                                                                                      \
   if (hd == HDV) {                                                                                                  \
-    hipLaunchKernelGGL((gnorm_gate_bwd_rows_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)y,            \
+    HDCM_LAUNCH((gnorm_gate_bwd_rows_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)y,            \
                        y_row_stride, (const TT*)gate, gate_row_stride, (const TT*)gn_w, (const TT*)gn_b, eps,       \
                        (const TT*)dout, dout_row_stride, (TT*)dy, dy_row_stride, (TT*)dgate, dgate_row_stride,      \
                        (float*)ws, rows, (int)dm, nstripe);                                                         \
@@ -346,7 +346,7 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
     const dim3 grid((unsigned)(nwaves / kWaves));
 #define HDCM_GNG_CASE(TT, HDV)                                                                                      \
   if (hd == HDV) {                                                                                                  \
-    hipLaunchKernelGGL((gnorm_gate_bwd_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)y, y_row_stride,     \
+    HDCM_LAUNCH((gnorm_gate_bwd_kernel<TT, HDV>), grid, dim3(kThreads), 0, s, (const TT*)y, y_row_stride,     \
                        (const TT*)gate, gate_row_stride, (const TT*)gn_w, (const TT*)gn_b, eps, (const TT*)dout,    \
                        dout_row_stride, (TT*)dy, dy_row_stride, (TT*)dgate, dgate_row_stride, (float*)ws, rows,     \
                        (int)H);                                                                                     \
@@ -383,10 +383,10 @@ extern "C" int hdcm_slot_phi_prep(const void* projs, int64_t proj_row_stride, in
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(grid_for(rows * (dm / E)));
   if (dtype == HDCM_F32)
-    hipLaunchKernelGGL((phi_prep_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs, proj_row_stride,
+    HDCM_LAUNCH((phi_prep_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs, proj_row_stride,
                        (int)q_col, (float*)z, z_row_stride, rows, (int)dm);
   else
-    hipLaunchKernelGGL((phi_prep_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs, proj_row_stride,
+    HDCM_LAUNCH((phi_prep_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs, proj_row_stride,
                        (int)q_col, (bf16_t*)z, z_row_stride, rows, (int)dm);
   return hdcm_launch_status();
 }
@@ -405,10 +405,10 @@ extern "C" int hdcm_slot_phi_chain(const void* projs, int64_t proj_row_stride, i
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(grid_for(rows * (2 * dm / E)));
   if (dtype == HDCM_F32)
-    hipLaunchKernelGGL((phi_chain_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs, proj_row_stride,
+    HDCM_LAUNCH((phi_chain_kernel<float>), grid, dim3(kThreads), 0, s, (const float*)projs, proj_row_stride,
                        (int)q_col, (float*)dprojs, dprojs_row_stride, rows, (int)dm);
   else
-    hipLaunchKernelGGL((phi_chain_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs, proj_row_stride,
+    HDCM_LAUNCH((phi_chain_kernel<bf16_t>), grid, dim3(kThreads), 0, s, (const bf16_t*)projs, proj_row_stride,
                        (int)q_col, (bf16_t*)dprojs, dprojs_row_stride, rows, (int)dm);
   return hdcm_launch_status();
 }

@@ -208,16 +208,16 @@ int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, v
   float* th = ta + n;
   float* hin = th + n;
   const dim3 grid((unsigned)nt, (unsigned)((ds + kCh - 1) / kCh), (unsigned)B);
-  hipLaunchKernelGGL((ssm_tile_kernel<T, false, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+  HDCM_LAUNCH((ssm_tile_kernel<T, false, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
                      (const T*)A_log, ta, th, (const float*)nullptr, (T*)nullptr, (int64_t)0,
                      (float*)nullptr, (int)L, (int)ds, (int)nt, (const T*)nullptr, (int64_t)0);
   int st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th, h0,
+  HDCM_LAUNCH(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th, h0,
                      hin, h_final, (int)ds, (int)nt);
   st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL((ssm_tile_kernel<T, true, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+  HDCM_LAUNCH((ssm_tile_kernel<T, true, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
                      (const T*)A_log, (float*)nullptr, (float*)nullptr, hin, (T*)y, yrs,
                      (float*)nullptr, (int)L, (int)ds, (int)nt, (const T*)nullptr, (int64_t)0);
   return hdcm_launch_status();
@@ -230,10 +230,10 @@ extern "C" size_t hdcm_ssm_workspace_bytes(int64_t B, int64_t L, int64_t ds) {
   return (size_t)(3 * B * ssm_tiles(L) * ds) * sizeof(float);
 }
 
-extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
-                            const float* h0, void* y, int64_t y_row_stride, float* h_final,
-                            void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds, int dtype,
-                            void* stream) {
+// Argument checks of the forward entry points, everything but the workspace (also used by
+// other sources of the library that run these kernels).
+int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const void* y,
+                       int64_t y_row_stride, int64_t B, int64_t L, int64_t ds, int dtype) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(A_log && ((projs && y) || B == 0 || L == 0), HDCM_EINVAL);  // empty: NULL data allowed
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && ds > 0, HDCM_EINVAL);
@@ -242,15 +242,30 @@ extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const vo
   HDCM_CHECK_ARG(ds % E == 0 && proj_row_stride % E == 0 && y_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(hdcm_aligned16(projs) && hdcm_aligned16(y) && hdcm_aligned16(A_log), HDCM_EALIGN);
   HDCM_CHECK_ARG(B <= 65535 && ssm_tiles(L) < ((int64_t)1 << 31) && ds <= 65535, HDCM_EUNSUPPORTED);
+  return HDCM_OK;
+}
+
+// The forward's launches on a checked, non-empty input with a workspace of
+// hdcm_ssm_workspace_bytes(B, L, ds) bytes at `ws` (4-byte aligned).
+int hdcm_ssm_launch_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const float* h0, void* y,
+                        int64_t y_row_stride, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds, int dtype,
+                        hipStream_t s) {
+  if (dtype == HDCM_F32)
+    return launch<float>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, s);
+  return launch<bf16_t>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, s);
+}
+
+extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
+                            const float* h0, void* y, int64_t y_row_stride, float* h_final,
+                            void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds, int dtype,
+                            void* stream) {
+  const int st = hdcm_ssm_check_fwd(projs, proj_row_stride, A_log, y, y_row_stride, B, L, ds, dtype);
+  if (st) return st;
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_ssm_workspace_bytes(B, L, ds), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 3u) == 0, HDCM_EALIGN);
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == HDCM_F32)
-    return launch<float>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds,
-                         s);
-  return launch<bf16_t>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds,
-                        s);
+  return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, dtype,
+                             (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------- backward
@@ -346,23 +361,23 @@ int launch_bwd(const void* projs, int64_t prs, const void* A_log, const void* h,
   T* g = (T*)((char*)ws + align256((size_t)3 * n * sizeof(float)));
   float* part = (float*)((char*)g + align256((size_t)B * L * ds * sizeof(T)));
   const dim3 grid((unsigned)nt, (unsigned)((ds + kCh - 1) / kCh), (unsigned)B);
-  hipLaunchKernelGGL((ssm_tile_kernel<T, false, true>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+  HDCM_LAUNCH((ssm_tile_kernel<T, false, true>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
                      (const T*)A_log, ta, th, (const float*)nullptr, (T*)nullptr, (int64_t)0, (float*)nullptr,
                      (int)L, (int)ds, (int)nt, (const T*)gy, gyrs);
   int st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th,
+  HDCM_LAUNCH(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th,
                      (const float*)nullptr, hin, (float*)nullptr, (int)ds, (int)nt);
   st = hdcm_launch_status();
   if (st) return st;
-  hipLaunchKernelGGL((ssm_tile_kernel<T, true, true>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
+  HDCM_LAUNCH((ssm_tile_kernel<T, true, true>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
                      (const T*)A_log, (float*)nullptr, (float*)nullptr, hin, g, ds, (float*)nullptr, (int)L,
                      (int)ds, (int)nt, (const T*)gy, gyrs);
   st = hdcm_launch_status();
   if (st) return st;
   const int64_t nb = grad_blocks(B * L, ds, E);
   const int rows_per = (int)(kThreads / (ds / E));
-  hipLaunchKernelGGL((ssm_grad_kernel<T>), dim3((unsigned)nb), dim3(kThreads),
+  HDCM_LAUNCH((ssm_grad_kernel<T>), dim3((unsigned)nb), dim3(kThreads),
                      (size_t)rows_per * ds * sizeof(float), s, (const T*)projs, prs, (const T*)A_log, (const T*)h,
                      hrs, (const T*)g, ds, (T*)dprojs, dprs, part, B * L, (int)L, (int)ds);
   st = hdcm_launch_status();

@@ -49,6 +49,20 @@ int hdcm_abi_version(void);
 const char* hdcm_strerror(int status);
 
 /*
+ * Kernel timing for measurement harnesses.  Arms the calling thread: the k-th kernel
+ * (k < n) that the following hdcm_* calls of this thread launch records start_events[k] when
+ * it begins and stop_events[k] when it ends (hipEvent_t handles, created by the caller),
+ * from the dispatch's own begin/end timestamps (hipExtLaunchKernel), so no event packets
+ * enter the stream.  The arrays must stay valid while armed; n = 0 disarms.
+ * hdcm_timed_launch_count returns how many launches have recorded events since arming.
+ * Not for calls made under stream capture.
+ * No counterpart in the reference (benchmark.py:165-192 times whole forwards with
+ * torch.cuda.synchronize around them).
+ */
+int hdcm_time_launches(void* const* start_events, void* const* stop_events, int n);
+int hdcm_timed_launch_count(void);
+
+/*
  * LayerNorm over D (biased variance, eps) followed by the causal depthwise
  * conv of width 4: out[t] = sum_k LN(x)[t-3+k] * conv_w[:,k] + conv_b, with
  * LN rows t<0 equal to ln_b (LayerNorm of a zero row).
@@ -126,7 +140,7 @@ int hdcm_ssm_bwd(const void* projs, int64_t proj_row_stride, const void* A_log, 
  * (gn_eps, affine gn_w/gn_b [dm]) times sigmoid(gate), written to columns
  * [out_col, out_col+dm) of `out`; S_final [B,H,hd,hd] fp32 (or NULL) receives
  * the state after row L-1 (L must then be a multiple of C).
- * Needs hd in {32,64,96}; C a power of two dividing the row tile (64 rows
+ * Needs hd in {32,64,96,128}; C a power of two dividing the row tile (64 rows
  * for bf16, 32 for fp32) or a multiple of it; L a multiple of C.
  * Replaces: _slot_all_fused launch (hdcmamba/model.py:366-371, kernel
  *           model.py:236-272) and the slot part of _fused_gnorm_gate_cat_kernel

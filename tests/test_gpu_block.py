@@ -46,6 +46,25 @@ def test_block_padding(dev, dtype, L, C):
     assert_close(y, ref, dtype, f"pad L={L} C={C}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_block_default_heads_hd128(dev, dtype):
+    """d_model 1024 with the constructor's default num_heads=8 (head dim 128), the shape a
+    plain HdcMamba9v3Model(1024, n, 128, slots) builds."""
+    print("block hd128", dtype, flush=True)
+    from hdcmamba_amd import HdcMamba9v3Block
+    from cfgs import reinit_block_
+
+    torch.manual_seed(11)
+    blk = reinit_block_(HdcMamba9v3Block(1024, 128, chunk_size=64), seed=11).eval().to(dtype)
+    assert blk.head_dim == 128
+    x = torch.randn(1, 320, 1024, generator=torch.Generator().manual_seed(12)).to(dtype)
+    ref = oracle.block_forward(_sd(blk), x, oracle_cfg(blk))
+    with torch.no_grad():
+        y, _ = blk.to(dev)(x.to(dev))
+    print("max rel", max_rel(y, ref), flush=True)
+    assert_close(y, ref, dtype, f"hd128 {dtype}")
+
+
 def test_model_and_lm_small(dev):
     """2-layer LM (d_model 768, heads 12) at B=2, L=512 through embedding, blocks, norms, tied head."""
     print("lm small", flush=True)

@@ -111,6 +111,10 @@ SLOT_CASES = [
     (torch.bfloat16, 1, 512, 512, 8, 32),
     (torch.bfloat16, 1, 512, 512, 8, 256),
     (torch.bfloat16, 2, 96, 256, 4, 32),     # last row tile half full (32 of 64 rows)
+    (torch.float32, 1, 256, 512, 4, 64),     # hd 128
+    (torch.float32, 1, 256, 512, 4, 16),     # hd 128, C < TC
+    (torch.bfloat16, 2, 320, 1024, 8, 64),   # hd 128 (d_model 1024 with the default 8 heads)
+    (torch.bfloat16, 1, 512, 512, 4, 128),   # hd 128, C > TC
 ]
 
 
@@ -166,6 +170,8 @@ ATTEND_CASES = [
     (torch.bfloat16, 1, 256, 512, 8, 32),    # C < row tile
     (torch.float32, 1, 256, 256, 4, 128),    # C > row tile: carried within-chunk state
     (torch.bfloat16, 1, 256, 768, 8, 128),   # hd 96
+    (torch.bfloat16, 1, 256, 1024, 8, 64),   # hd 128
+    (torch.float32, 1, 128, 512, 4, 32),     # hd 128
 ]
 
 
