@@ -31,6 +31,8 @@ _PROTOS = {
     "hdcm_ssm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "hdcm_ssm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
                              c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_ssm_fwd_noalloc": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
+                                     c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_ssm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
     "hdcm_ssm_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
@@ -326,6 +328,24 @@ def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
         y.data_ptr(), yrs, h_final.data_ptr() if h_final is not None else None, ws.data_ptr(), nbytes,
         B, L, d_state, _dtype(projs), _stream(projs)))
     timer.end("ssm", ev)
+    return y
+
+
+def ssm_noalloc(projs, A_log, d_state, y, h0=None, h_final=None):
+    """ssm() on the library's fixed per-GPU scratch instead of an allocated workspace
+    (hdcm_ssm_fwd_noalloc): this wrapper and the call allocate nothing on the device.
+    Calls that overlap on one GPU share the scratch and race."""
+    _on_gpu(projs, y)
+    B, L, _ = projs.shape
+    if A_log.dtype != projs.dtype or A_log.device != projs.device or not A_log.is_contiguous():
+        raise RuntimeError("ssm_noalloc: A_log must be a contiguous tensor of projs' dtype and device")
+    for name, t in (("h0", h0), ("h_final", h_final)):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise RuntimeError(f"ssm_noalloc: {name} must be a contiguous fp32 tensor")
+    _check("hdcm_ssm_fwd_noalloc", lib().hdcm_ssm_fwd_noalloc(
+        projs.data_ptr(), _rows2d(projs, "projs"), A_log.data_ptr(), h0.data_ptr() if h0 is not None else None,
+        y.data_ptr(), _rows2d(y, "y"), h_final.data_ptr() if h_final is not None else None, B, L, d_state,
+        _dtype(projs), _stream(projs)))
     return y
 
 

@@ -22,6 +22,7 @@ extern "C" const char* hdcm_strerror(int status) {
     case HDCM_EUNSUPPORTED: return "unsupported dtype/shape combination";
     case HDCM_ELAUNCH: return "HIP kernel launch failed";
     case HDCM_EWORKSPACE: return "workspace missing or too small";
+    case HDCM_ETOOBIG: return "input exceeds the fixed scratch of the no-allocation entry point";
     default: return "unknown hdcm status";
   }
 }

@@ -40,7 +40,8 @@ typedef enum {
   HDCM_EALIGN = -2,       /* pointer or row stride not 16-byte aligned */
   HDCM_EUNSUPPORTED = -3, /* valid but not built: dtype/head_dim/chunk combination */
   HDCM_ELAUNCH = -4,      /* a HIP launch reported an error */
-  HDCM_EWORKSPACE = -5    /* workspace missing or smaller than required */
+  HDCM_EWORKSPACE = -5,   /* workspace missing or smaller than required */
+  HDCM_ETOOBIG = -6       /* input larger than a no-allocation entry point's fixed scratch */
 } hdcm_status;
 
 #define HDCM_ABI_VERSION 1
@@ -110,6 +111,22 @@ int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
                  const float* h0, void* y, int64_t y_row_stride, float* h_final,
                  void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds,
                  int dtype, void* stream);
+
+/*
+ * hdcm_ssm_fwd without a workspace argument: the same kernels and results, with their
+ * scratch in a fixed device array of HDCM_SSM_NOALLOC_SCRATCH_BYTES that the library holds on
+ * each GPU it runs on until the process ends.  The call allocates nothing (no hipMalloc, no
+ * allocating library routine), so it can be used where allocation is not possible.  Inputs
+ * whose workspace (hdcm_ssm_workspace_bytes) would exceed that size return HDCM_ETOOBIG.
+ * Every call on one GPU uses that GPU's array: calls that overlap on one GPU (concurrent
+ * streams) race; calls ordered on one stream do not.
+ * No counterpart in the reference; for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid allocation).
+ */
+#define HDCM_SSM_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int hdcm_ssm_fwd_noalloc(const void* projs, int64_t proj_row_stride, const void* A_log,
+                         const float* h0, void* y, int64_t y_row_stride, float* h_final,
+                         int64_t B, int64_t L, int64_t ds, int dtype, void* stream);
 
 /*
  * Gradient of hdcm_ssm_fwd from a zero start state: given gy (the gradient of y) and h (the

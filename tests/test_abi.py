@@ -10,7 +10,7 @@ import torch
 from hdcmamba_amd import _ops
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "hdcm.h"
-OK, EINVAL, EALIGN, EUNSUPPORTED, ELAUNCH, EWORKSPACE = 0, -1, -2, -3, -4, -5
+OK, EINVAL, EALIGN, EUNSUPPORTED, ELAUNCH, EWORKSPACE, ETOOBIG = 0, -1, -2, -3, -4, -5, -6
 
 
 def declared():
@@ -75,6 +75,23 @@ def test_ssm_validation():
     assert f(*a) == EINVAL
     a = list(base); a[0] = P17
     assert f(*a) == EALIGN
+
+
+def test_ssm_noalloc_validation():
+    """The no-allocation scan checks like hdcm_ssm_fwd and rejects inputs whose scratch would
+    exceed its fixed array before any HIP call."""
+    f = _ops.lib().hdcm_ssm_fwd_noalloc
+    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, 1, 256, 64, 1, None]
+    a = list(base); a[1] = 100
+    assert f(*a) == EINVAL
+    a = list(base); a[0] = P17
+    assert f(*a) == EALIGN
+    a = list(base); a[7] = 0
+    assert f(*a) == OK  # empty: nothing to do
+    a = list(base); a[7], a[8], a[9] = 64, 32768, 128  # 48 MiB of scratch
+    a[1], a[5] = 3 * 128, 128
+    assert f(*a) == ETOOBIG
+    assert b"scratch" in _ops.lib().hdcm_strerror(ETOOBIG)
 
 
 def test_slot_validation():

@@ -1,0 +1,54 @@
+"""hdcm_ssm_fwd_noalloc (the scan on the library's fixed per-GPU scratch) through the C ABI
+against hdcm_ssm_fwd (the same kernels on an allocated workspace): two calls in a row, the
+second on a smaller input, each bit-identical to the workspace entry point's result."""
+import pytest
+import torch
+
+from cfgs import ssm_inputs
+from hdcmamba_amd import _ops
+
+pytestmark = pytest.mark.gpu
+
+ETOOBIG = -6
+
+
+def _call(fn_name, projs, A_log, ds, y, hf, ws=None):
+    lib = _ops.lib()
+    B, L, P = projs.shape
+    stream = torch.cuda.current_stream(projs.device).cuda_stream
+    args = [projs.data_ptr(), P, A_log.data_ptr(), None, y.data_ptr(), y.stride(1), hf.data_ptr()]
+    if ws is not None:
+        args += [ws.data_ptr(), ws.numel()]
+    args += [B, L, ds, _ops._dtype(projs), stream]
+    return getattr(lib, fn_name)(*args)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_matches_workspace_entry_point(dev, dtype):
+    lib = _ops.lib()
+    for B, L, ds in ((2, 1000, 128), (1, 300, 64)):  # the second call is smaller
+        print("ssm noalloc", dtype, B, L, ds, flush=True)
+        projs, A_log = ssm_inputs(B, L, ds, dtype, seed=L)
+        projs, A_log = projs.to(dev), A_log.to(dev)
+        y_ref = torch.zeros(B, L, ds + 8, device=dev, dtype=dtype)
+        hf_ref = torch.zeros(B, ds, device=dev)
+        ws = torch.empty(lib.hdcm_ssm_workspace_bytes(B, L, ds), dtype=torch.uint8, device=dev)
+        assert _call("hdcm_ssm_fwd", projs, A_log, ds, y_ref[..., :ds], hf_ref, ws) == 0
+        y = torch.zeros_like(y_ref)
+        hf = torch.zeros_like(hf_ref)
+        assert _call("hdcm_ssm_fwd_noalloc", projs, A_log, ds, y[..., :ds], hf) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), (y.float() - y_ref.float()).abs().max().item()
+        assert torch.equal(hf, hf_ref)
+        assert y[..., ds:].abs().max().item() == 0.0
+
+
+def test_noalloc_rejects_inputs_beyond_its_scratch(dev):
+    lib = _ops.lib()
+    B, L, ds = 64, 32768, 128  # needs 3*64*512*128*4 = 48 MiB of scratch
+    assert lib.hdcm_ssm_workspace_bytes(B, L, ds) > (8 << 20)
+    projs = torch.empty(16, dtype=torch.bfloat16, device=dev)  # never read: rejected first
+    st = lib.hdcm_ssm_fwd_noalloc(projs.data_ptr(), 3 * ds, projs.data_ptr(), None, projs.data_ptr(), ds, None,
+                                  B, L, ds, _ops.HDCM_BF16, torch.cuda.current_stream(dev).cuda_stream)
+    assert st == ETOOBIG
+    assert b"scratch" in lib.hdcm_strerror(st)
