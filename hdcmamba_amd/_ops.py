@@ -311,6 +311,28 @@ def norm_conv_bwd(grad_out, x, ln_w, ln_b, conv_w, eps):
     return dx, d_ln_w, d_ln_b, d_conv_w, d_conv_b
 
 
+_ssm_ws = {}       # (device index, stream) -> the scan's persistent workspace
+_ssm_ws_kept = []  # replaced workspaces stay allocated: a recorded graph may still use them
+
+
+def _ssm_workspace(device, nbytes):
+    """The scan's workspace for the current stream of `device`: zero-filled once, then reused
+    by every call on that stream (the kernel keeps it consistent; calls on one stream are
+    ordered, calls on different streams get different workspaces)."""
+    stream = torch.cuda.current_stream(device)
+    key = (stream.device.index, stream.cuda_stream)
+    ws = _ssm_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("ssm: the scan's workspace must exist before graph capture; run the "
+                               "forward once outside capture first")
+        if ws is not None:
+            _ssm_ws_kept.append(ws)
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _ssm_ws[key] = ws
+    return ws
+
+
 def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
     """Selective scan; writes y [B,L,ds] (may be a column slice of a wider buffer)."""
     _on_gpu(projs, y)
@@ -319,7 +341,7 @@ def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
     prs = _rows2d(projs, "projs")
     yrs = _rows2d(y, "y")
     nbytes = lib().hdcm_ssm_workspace_bytes(B, L, d_state)
-    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=projs.device)
+    ws = _ssm_workspace(projs.device, nbytes)
     if h0 is not None:
         h0 = h0.float().contiguous()
     ev = timer.begin("ssm")

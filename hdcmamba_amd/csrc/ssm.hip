@@ -7,15 +7,33 @@
 // All state is fp32; y is rounded once to the activation dtype.
 //
 // The recurrence is the associative scan of pairs (a, u) under
-//   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2),
-// so a wave scans 64 consecutive rows of one channel with lanes = rows in six
-// shuffle steps instead of a 64-step serial loop.  Rows are cut into tiles of 64:
-//   1. ssm_tile_kernel<SUMMARY>: stage a tile's dt/x/b for 64 channels through LDS as
-//      (a, u) pairs, scan each channel, keep the tile total (A, H) [b][channel][tile].
-//   2. ssm_carry_kernel: per channel, scan the tile totals (lanes = groups of tiles) to
-//      get the state entering every tile, h_in[b][channel][tile], and h_final.
-//   3. ssm_tile_kernel<OUTPUT>: rescan each tile, y_t = U_t + A_t * h_in, staged back
+//   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2).
+//
+// Forward (ssm_scan_kernel): one launch that reads every input once.  A workgroup owns a
+// tile of TR rows x 64 channels.  A thread holds 8 consecutive rows x one 16-byte channel
+// group, scans them serially in registers, and the row groups are combined by a lane scan
+// (shuffles) and across waves through LDS.  The workgroup then publishes its tile total
+// (A, H) per channel and folds the totals of all earlier tiles of its sequence into the
+// state entering the tile (decoupled look-back over totals, no inclusive chain), applies it
+// to the rows it still holds in registers and stores y once.  Totals are published as 64-bit
+// agent-scope atomic words {value, tag} that bypass the non-coherent per-XCD L2s, one word
+// for A and one for H, so a reader needs no fence: a word is valid when its tag is this
+// call's.  The tag is an epoch kept in the workspace header, read by every workgroup at its
+// start and advanced by the last workgroup to finish, so the workspace never needs clearing
+// (it must be zero before its first use).  A workgroup that finds an earlier total missing
+// polls for a bounded number of rounds, then computes that tile's total itself with the
+// same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
+// whatever order the workgroups run in.
+//
+// Backward (the adjoint scan, reversed rows): the three-pass form below.
+//   1. ssm_tile_kernel<SUMMARY>: stage a tile's (a, u) pairs for 64 channels through LDS,
+//      scan each channel with lanes = rows, keep the tile total (A, H) [b][channel][tile].
+//   2. ssm_carry_kernel: per channel, scan the tile totals to get the state entering every
+//      tile, h_in[b][channel][tile].
+//   3. ssm_tile_kernel<OUTPUT>: rescan each tile, out_t = U_t + A_t * h_in, staged back
 //      through LDS for 128-bit row stores.
+#include <stdlib.h>
+
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -198,28 +216,440 @@ __global__ __launch_bounds__(kWave) void ssm_carry_kernel(const float* __restric
 
 inline int64_t ssm_tiles(int64_t L) { return (L + kTile - 1) / kTile; }
 
+// ------------------------------------------------------------- single-pass forward
+// 512 threads x 4 rows: at the 32768-row, 128-channel shape 25.8 us against 30.0 us for
+// 256 x 8 and 35.7 us for 512 x 8 (which spills), measured in isolation.
+constexpr int kScanThreads = 512;
+constexpr int kScanCh = 64;  // channels per workgroup
+constexpr int kRPT = 4;      // rows per thread
+constexpr int kScanWaves = kScanThreads / kWave;
+constexpr int kHeaderBytes = 256;  // workspace header: epoch, finished-workgroup count
+constexpr int kDefaultSpinRounds = 256;
+constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
+constexpr int kCachePolicySC1 = 16;       // buffer load cache policy: agent-scope coherent (sc1)
+
+template <typename T>
+struct ScanShape {
+  static constexpr int E = Vec<T>::N;           // channels per thread (one 16-byte group)
+  static constexpr int CG = kScanCh / E;        // channel groups per tile
+  static constexpr int RG = kScanThreads / CG;  // row groups per tile
+  static constexpr int TR = RG * kRPT;          // rows per tile: 256 (bf16), 128 (fp32)
+};
+
+// Largest tile count any dtype needs for L rows (the fp32 tiles are the shorter ones).
+inline int64_t scan_tiles_max(int64_t L) { return (L + ScanShape<float>::TR - 1) / ScanShape<float>::TR; }
+
+// Workspace layout: header (epoch, finished-workgroup count), then the tile totals: per
+// sequence (batch row x channel block), channel and tile one 16-byte (A, H) pair of tagged
+// words.
+struct ScanWorkspace {
+  int64_t words_at, words_bytes;
+};
+inline ScanWorkspace scan_workspace(int64_t B, int64_t L, int64_t ds) {
+  const int64_t nseq = B * ((ds + kScanCh - 1) / kScanCh);
+  ScanWorkspace w;
+  w.words_at = kHeaderBytes;
+  w.words_bytes = nseq * kScanCh * scan_tiles_max(L) * 16;
+  return w;
+}
+
+__device__ __forceinline__ unsigned long long pack_word(float v, unsigned tag) {
+  return ((unsigned long long)tag << 32) | (unsigned long long)__float_as_uint(v);
+}
+__device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((unsigned)w); }
+__device__ __forceinline__ unsigned word_tag(unsigned long long w) { return (unsigned)(w >> 32); }
+
+// Row r (< kRPT) of this thread's rows of a tile (tile*TR + rg*kRPT + r, clamped to L-1:
+// rows past L are re-read and masked later) at its channel group (group 0 past nch).
+template <typename T>
+__device__ __forceinline__ const T* row_ptr(const T* __restrict__ projs, int64_t prs, int64_t rowbase, int tile,
+                                            int c0, int nch, int L, int r) {
+  using S = ScanShape<T>;
+  const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
+  const int t = min(tile * S::TR + rg * kRPT + r, L - 1);
+  return projs + (rowbase + t) * prs + (cg * S::E < nch ? c0 + cg * S::E : 0);
+}
+
+// This thread's rows x E channels of dt, x, b, as stored: every thread issues the same
+// 3*kRPT loads.
+template <typename T>
+__device__ __forceinline__ void load_rows(const T* __restrict__ projs, int64_t prs, int64_t rowbase, int tile, int c0,
+                                          int nch, int L, int ds, uint4 (&raw)[kRPT][3]) {
+#pragma unroll
+  for (int r = 0; r < kRPT; ++r) {
+    const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
+    raw[r][0] = ldg16(p);
+    raw[r][1] = ldg16(p + ds);
+    raw[r][2] = ldg16(p + 2 * ds);
+  }
+}
+
+// The pairs (a, u) of one row from its dt, x, b groups; the identity (1, 0) when !ok (rows
+// past L, channels past nch).
+template <typename T>
+__device__ __forceinline__ void pairs_of(const uint4 (&g)[3], const float (&negA)[Vec<T>::N], bool ok,
+                                         float (&a)[Vec<T>::N], float (&u)[Vec<T>::N]) {
+  constexpr int E = Vec<T>::N;
+  float d[E], xv[E], bv[E];
+  unpack16<T>(g[0], d);
+  unpack16<T>(g[1], xv);
+  unpack16<T>(g[2], bv);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float dt = softplus20(d[e]);
+    a[e] = ok ? fexp(dt * negA[e]) : 1.f;
+    u[e] = ok ? (dt * bv[e]) * xv[e] : 0.f;
+  }
+}
+
+// One row folded into this thread's running total (ca, ch), rows in order.  Every
+// multiply-add here and in combine_tile is an explicit fmaf, so a tile total has identical
+// bits wherever it is computed (by the tile's owner, or by a workgroup computing it on the
+// owner's behalf with tile_total_streamed).
+template <typename T>
+__device__ __forceinline__ void fold_row(const uint4 (&g)[3], const float (&negA)[Vec<T>::N], bool ok,
+                                         float (&ca)[Vec<T>::N], float (&ch)[Vec<T>::N]) {
+  constexpr int E = Vec<T>::N;
+  float a[E], u[E];
+  pairs_of<T>(g, negA, ok, a, u);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    ch[e] = fmaf(a[e], ch[e], u[e]);
+    ca[e] = ca[e] * a[e];
+  }
+}
+
+// LDS of the cross-thread part of a tile: one (A, H) pair per row group and channel, the
+// segment totals, and the tile total.
+constexpr int kMaxRG = kScanThreads / (kScanCh / 8);  // row groups of the bf16 tile (the most)
+constexpr int kSeg = kScanThreads / kScanCh;          // row-group segments, one thread per channel each
+struct ScanLds {
+  float rg[kMaxRG][kScanCh][2];
+  float seg[kSeg][kScanCh][2];
+  float tot[kScanCh][2];
+};
+
+template <typename T>
+__device__ __forceinline__ void combine_tile(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N], int nch,
+                                             float (&xa)[Vec<T>::N], float (&xh)[Vec<T>::N], float (&ta)[Vec<T>::N],
+                                             float (&th)[Vec<T>::N], ScanLds* lds);
+
+// A tile's total (threads of row group 0: their E channels) with the rows read one at a time
+// (few registers in use): the kernel's own fold, row by row in the same order, then
+// combine_tile, hence the same bits.
+template <typename T>
+__device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs, int64_t prs, int64_t rowbase,
+                                                    int tile, int c0, int nch, int L, int ds,
+                                                    const float (&negA)[Vec<T>::N], float (&ta)[Vec<T>::N],
+                                                    float (&th)[Vec<T>::N], ScanLds* lds) {
+  using S = ScanShape<T>;
+  constexpr int E = S::E;
+  const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
+  const bool cok = cg * E < nch;
+  const int r0 = tile * S::TR + rg * kRPT;
+  float ca[E], ch[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) ca[e] = 1.f, ch[e] = 0.f;
+#pragma unroll 1
+  for (int r = 0; r < kRPT; ++r) {
+    const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
+    const uint4 g[3] = {ldg16(p), ldg16(p + ds), ldg16(p + 2 * ds)};
+    fold_row<T>(g, negA, cok && r0 + r < L, ca, ch);
+  }
+  float xa[E], xh[E];
+  combine_tile<T>(ca, ch, nch, xa, xh, ta, th, lds);
+}
+
+// The cross-thread part of a tile, from each thread's total (ca, ch) over its rows: the row
+// groups' pairs go to LDS, thread (segment s, channel c) folds its run of row groups in
+// order, the segment totals are folded in order, and each row group gets back its exclusive
+// prefix.  Yields this thread's exclusive prefix (xa, xh) within the tile and (threads of
+// row group 0) the tile total (ta, th) of their E channels.
+template <typename T>
+__device__ __forceinline__ void combine_tile(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N], int nch,
+                                             float (&xa)[Vec<T>::N], float (&xh)[Vec<T>::N], float (&ta)[Vec<T>::N],
+                                             float (&th)[Vec<T>::N], ScanLds* lds) {
+  using S = ScanShape<T>;
+  constexpr int E = S::E, CG = S::CG, RG = S::RG;
+  constexpr int RGS = RG / kSeg;  // row groups per segment
+  static_assert(RG % kSeg == 0 && RG <= kMaxRG, "row-group segments");
+  const int tid = threadIdx.x, cg = tid % CG, rg = tid / CG;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    lds->rg[rg][cg * E + e][0] = ca[e];
+    lds->rg[rg][cg * E + e][1] = ch[e];
+  }
+  __syncthreads();
+  const int c = tid % kScanCh, s = tid / kScanCh;
+  float va[RGS], vh[RGS];
+  float sa = 1.f, sh = 0.f;
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    va[k] = lds->rg[s * RGS + k][c][0];
+    vh[k] = lds->rg[s * RGS + k][c][1];
+  }
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    sh = fmaf(va[k], sh, vh[k]);
+    sa = sa * va[k];
+  }
+  lds->seg[s][c][0] = sa;
+  lds->seg[s][c][1] = sh;
+  __syncthreads();
+  float pa = 1.f, ph = 0.f;  // segments before s
+  for (int k = 0; k < s; ++k) {
+    const float ka = lds->seg[k][c][0], kh = lds->seg[k][c][1];
+    ph = fmaf(ka, ph, kh);
+    pa = pa * ka;
+  }
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    lds->rg[s * RGS + k][c][0] = pa;
+    lds->rg[s * RGS + k][c][1] = ph;
+    ph = fmaf(va[k], ph, vh[k]);
+    pa = pa * va[k];
+  }
+  if (s == kSeg - 1) {
+    lds->tot[c][0] = pa;
+    lds->tot[c][1] = ph;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    xa[e] = lds->rg[rg][cg * E + e][0];
+    xh[e] = lds->rg[rg][cg * E + e][1];
+    ta[e] = rg == 0 ? lds->tot[cg * E + e][0] : 1.f;
+    th[e] = rg == 0 ? lds->tot[cg * E + e][1] : 0.f;
+  }
+  __syncthreads();  // the LDS is reused
+}
+
+// The tile total of this thread's channels, published for later tiles (row group 0 only).
+template <typename T>
+__device__ __forceinline__ void publish_total(unsigned long long* words, int64_t seq, int ntiles, int tile,
+                                              int nch, const float (&ta)[Vec<T>::N], const float (&th)[Vec<T>::N],
+                                              unsigned tag) {
+  using S = ScanShape<T>;
+  const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
+  if (rg != 0) return;
+#pragma unroll
+  for (int e = 0; e < S::E; ++e) {
+    const int c = cg * S::E + e;
+    if (c >= nch) continue;
+    unsigned long long* p = words + 2 * ((seq * kScanCh + c) * ntiles + tile);
+    __hip_atomic_store(p, pack_word(ta[e], tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, pack_word(th[e], tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Compute and publish, with this call's tag, the totals of the tiles j0 + k for the set bits
+// k of `missing` (the rare path of the look-back).  All threads of the workgroup call it
+// together.
+template <typename T>
+__device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int64_t prs,
+                                                const float (&negA)[Vec<T>::N], unsigned long long* words, int64_t seq,
+                                                int64_t rowbase, int c0, int nch, int L, int ds, int ntiles, int j0,
+                                                unsigned long long missing, unsigned tag, ScanLds* lds) {
+  constexpr int E = Vec<T>::N;
+  while (missing != 0) {
+    const int jm = j0 + __builtin_ctzll(missing);
+    missing &= missing - 1;
+    float ta[E], th[E];
+    tile_total_streamed<T>(projs, prs, rowbase, jm, c0, nch, L, ds, negA, ta, th, lds);
+    publish_total<T>(words, seq, ntiles, jm, nch, ta, th, tag);
+  }
+}
+
+// One workgroup per (tile, 64-channel block, sequence).  See the file header.
+template <typename T>
+__global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
+    const T* __restrict__ projs, int64_t prs, const T* __restrict__ A_log, const float* __restrict__ h0,
+    T* __restrict__ y, int64_t yrs, float* __restrict__ h_final, unsigned* __restrict__ hdr,
+    unsigned long long* __restrict__ words, int words_bytes, int L, int ds, int ntiles, int spin_rounds) {
+  using S = ScanShape<T>;
+  constexpr int E = S::E, CG = S::CG;
+  constexpr int CPW = kScanCh / kScanWaves;  // look-back channels per wave
+  __shared__ ScanLds s_lds;
+  __shared__ float s_hin[kScanCh];
+  __shared__ unsigned s_missing[kScanWaves][2];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int cg = tid % CG, rg = tid / CG;
+  const int tile = blockIdx.x, chb = blockIdx.y, b = blockIdx.z;
+  const int c0 = chb * kScanCh;
+  const int nch = min(kScanCh, ds - c0);
+  const bool cok = cg * E < nch;
+  const int64_t seq = (int64_t)b * gridDim.y + chb;  // this tile's sequence of totals
+  const int64_t rowbase = (int64_t)b * L;
+  const unsigned tag = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+
+  float negA[E];
+  {
+    float al[E] = {};
+    if (cok) load16<T>(A_log + c0 + cg * E, al);
+#pragma unroll
+    for (int e = 0; e < E; ++e) negA[e] = -fexp(al[e]);
+  }
+  // this thread's rows: the prefixes (At, Ut) of its own rows, kept for the outputs, then the
+  // tile's exclusive prefix and total
+  float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E], ta[E], th[E];
+  {
+    uint4 raw[kRPT][3];
+    load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
+    const int r0 = tile * S::TR + rg * kRPT;
+    float ca[E], ch[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) ca[e] = 1.f, ch[e] = 0.f;
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) {
+      fold_row<T>(raw[r], negA, cok && r0 + r < L, ca, ch);
+#pragma unroll
+      for (int e = 0; e < E; ++e) At[r][e] = ca[e], Ut[r][e] = ch[e];
+    }
+    combine_tile<T>(ca, ch, nch, xa, xh, ta, th, &s_lds);
+  }
+  publish_total<T>(words, seq, ntiles, tile, nch, ta, th, tag);
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)words, (short)0, words_bytes, kBufferFlags);
+
+  // ---- state entering this tile: fold the totals of tiles 0 .. tile-1 (lanes = tiles, 64 at a
+  // time; wave w folds channels w*CPW .. +CPW-1), then apply to h0
+  float fa[CPW], fh[CPW];
+#pragma unroll
+  for (int k = 0; k < CPW; ++k) fa[k] = 1.f, fh[k] = 0.f;
+  // the (A, H) words of tile j0 + lane for this wave's channels: 16 bytes each, read through
+  // the buffer path with the agent-scope cache policy (coalesced, and never a stale L2 line;
+  // each 8-byte half carries its own tag, so a read torn between two stores shows a stale
+  // half and is read again)
+  auto read_window = [&](int j0, uint4 (&q)[CPW]) {
+    const int j = j0 + lane;
+#pragma unroll
+    for (int k = 0; k < CPW; ++k) {
+      const int c = w * CPW + k;
+      q[k] = make_uint4(0u, 0u, 0u, 0u);
+      if (j < tile && c < nch)
+        q[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             wrsrc, (int)(((seq * kScanCh + c) * ntiles + j) * 16), 0,
+                                             kCachePolicySC1));
+    }
+  };
+  for (int j0 = 0; j0 < tile; j0 += kWave) {
+    const int j = j0 + lane;
+    const bool act = j < tile;
+    uint4 q[CPW];
+    float va[CPW], vh[CPW];
+    for (int round = 0;; ++round) {
+      read_window(j0, q);
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < CPW; ++k) {
+        const int c = w * CPW + k;
+        va[k] = 1.f, vh[k] = 0.f;
+        if (act && c < nch) {
+          const unsigned long long wa = ((unsigned long long)q[k].y << 32) | q[k].x;
+          const unsigned long long wh = ((unsigned long long)q[k].w << 32) | q[k].z;
+          ok = ok && word_tag(wa) == tag && word_tag(wh) == tag;
+          va[k] = word_value(wa);
+          vh[k] = word_value(wh);
+        }
+      }
+      // tiles of this window that some wave still misses (one bit per lane)
+      const unsigned long long miss = __ballot(!ok);
+      if (lane == 0) {
+        s_missing[w][0] = (unsigned)miss;
+        s_missing[w][1] = (unsigned)(miss >> 32);
+      }
+      __syncthreads();
+      unsigned long long all = 0;
+#pragma unroll
+      for (int k = 0; k < kScanWaves; ++k)
+        all |= (unsigned long long)s_missing[k][0] | ((unsigned long long)s_missing[k][1] << 32);
+      __syncthreads();
+      // (the round cap only guarantees termination: after one computing pass every total of
+      // the window has been stored by this workgroup and is read back in the next round)
+      if (all == 0 || round > spin_rounds + 2) break;
+      if (round < spin_rounds) {
+        __builtin_amdgcn_s_sleep(4);
+        continue;
+      }
+      // still missing after the polling budget: compute those tiles' totals here and publish
+      // them for their owners (the owner's own store later writes the same bits)
+      publish_missing<T>(projs, prs, negA, words, seq, rowbase, c0, nch, L, ds, ntiles, j0, all, tag, &s_lds);
+      __syncthreads();
+    }
+    // fold this window in tile order: inclusive lane scan, the total sits in lane 63
+    scan_pairs<CPW>(va, vh);
+#pragma unroll
+    for (int k = 0; k < CPW; ++k) {
+      const float wa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(va[k]), kWave - 1));
+      const float wh = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vh[k]), kWave - 1));
+      fh[k] = fmaf(wa, fh[k], wh);
+      fa[k] = fa[k] * wa;
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < CPW; ++k) {
+      const int c = w * CPW + k;
+      const float hz = (h0 != nullptr && c < nch) ? h0[(int64_t)b * ds + c0 + c] : 0.f;
+      s_hin[c] = fmaf(fa[k], hz, fh[k]);
+    }
+  }
+  __syncthreads();
+
+  // ---- outputs: y_t = U_t + A_t * (state entering this thread's rows)
+  const int r0 = tile * S::TR + rg * kRPT;
+  float hs[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) hs[e] = fmaf(xa[e], s_hin[cg * E + e], xh[e]);
+  if (cok) {
+    T* yb = y + rowbase * yrs + c0 + cg * E;
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) {
+      const int t = r0 + r;
+      if (t >= L) break;
+      float v[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[e] = fmaf(At[r][e], hs[e], Ut[r][e]);
+      store16<T>(yb + (int64_t)t * yrs, v);
+      if (h_final != nullptr && t == L - 1) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) h_final[(int64_t)b * ds + c0 + cg * E + e] = v[e];
+      }
+    }
+  }
+
+  // ---- the last workgroup to finish advances the epoch (every workgroup has read its tag and
+  // finished its look-back by then) and resets the counts for the next call
+  if (tid == 0) {
+    const unsigned total = gridDim.x * gridDim.y * gridDim.z;
+    s_last = __hip_atomic_fetch_add(hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+  }
+  __syncthreads();
+  if (s_last && tid == 0) {
+    __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+int spin_rounds_setting() {
+  const char* v = getenv("HDCM_SSM_SPIN_ROUNDS");  // test hook: 0 forces the compute-it-here path
+  if (!v || !*v) return kDefaultSpinRounds;
+  const int x = atoi(v);
+  return x >= 0 ? x : kDefaultSpinRounds;
+}
+
 template <typename T>
 int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, void* y,
            int64_t yrs, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds,
            hipStream_t s) {
-  const int64_t nt = ssm_tiles(L);
-  const int64_t n = B * nt * ds;
-  float* ta = (float*)ws;
-  float* th = ta + n;
-  float* hin = th + n;
-  const dim3 grid((unsigned)nt, (unsigned)((ds + kCh - 1) / kCh), (unsigned)B);
-  HDCM_LAUNCH((ssm_tile_kernel<T, false, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
-                     (const T*)A_log, ta, th, (const float*)nullptr, (T*)nullptr, (int64_t)0,
-                     (float*)nullptr, (int)L, (int)ds, (int)nt, (const T*)nullptr, (int64_t)0);
-  int st = hdcm_launch_status();
-  if (st) return st;
-  HDCM_LAUNCH(ssm_carry_kernel, dim3((unsigned)ds, (unsigned)B), dim3(kWave), 0, s, ta, th, h0,
-                     hin, h_final, (int)ds, (int)nt);
-  st = hdcm_launch_status();
-  if (st) return st;
-  HDCM_LAUNCH((ssm_tile_kernel<T, true, false>), grid, dim3(kThreads), 0, s, (const T*)projs, prs,
-                     (const T*)A_log, (float*)nullptr, (float*)nullptr, hin, (T*)y, yrs,
-                     (float*)nullptr, (int)L, (int)ds, (int)nt, (const T*)nullptr, (int64_t)0);
+  const int64_t nt = (L + ScanShape<T>::TR - 1) / ScanShape<T>::TR;
+  const dim3 grid((unsigned)nt, (unsigned)((ds + kScanCh - 1) / kScanCh), (unsigned)B);
+  const ScanWorkspace w = scan_workspace(B, L, ds);
+  char* base = (char*)ws;
+  HDCM_LAUNCH((ssm_scan_kernel<T>), grid, dim3(kScanThreads), 0, s, (const T*)projs, prs, (const T*)A_log, h0, (T*)y,
+              yrs, h_final, (unsigned*)base, (unsigned long long*)(base + w.words_at), (int)w.words_bytes, (int)L,
+              (int)ds, (int)nt, spin_rounds_setting());
   return hdcm_launch_status();
 }
 
@@ -227,7 +657,8 @@ int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, v
 
 extern "C" size_t hdcm_ssm_workspace_bytes(int64_t B, int64_t L, int64_t ds) {
   if (B <= 0 || L <= 0 || ds <= 0) return 0;
-  return (size_t)(3 * B * ssm_tiles(L) * ds) * sizeof(float);
+  const ScanWorkspace w = scan_workspace(B, L, ds);
+  return (size_t)(w.words_at + w.words_bytes);
 }
 
 // Argument checks of the forward entry points, everything but the workspace (also used by
@@ -241,12 +672,16 @@ int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(ds % E == 0 && proj_row_stride % E == 0 && y_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(hdcm_aligned16(projs) && hdcm_aligned16(y) && hdcm_aligned16(A_log), HDCM_EALIGN);
-  HDCM_CHECK_ARG(B <= 65535 && ssm_tiles(L) < ((int64_t)1 << 31) && ds <= 65535, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(B <= 65535 && ds <= 65535 && L < ((int64_t)1 << 30), HDCM_EUNSUPPORTED);
+  // the scan kernel counts its workgroups, and addresses its tile totals, in 32 bits
+  HDCM_CHECK_ARG(B * ((ds + kScanCh - 1) / kScanCh) * scan_tiles_max(L) < ((int64_t)1 << 31) / (kScanCh * 16),
+                 HDCM_EUNSUPPORTED);
   return HDCM_OK;
 }
 
-// The forward's launches on a checked, non-empty input with a workspace of
-// hdcm_ssm_workspace_bytes(B, L, ds) bytes at `ws` (4-byte aligned).
+// The forward's launch on a checked, non-empty input with a workspace of
+// hdcm_ssm_workspace_bytes(B, L, ds) bytes at `ws` (256-byte aligned, zero before its first
+// use, then left as the previous call left it).
 int hdcm_ssm_launch_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const float* h0, void* y,
                         int64_t y_row_stride, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds, int dtype,
                         hipStream_t s) {
@@ -263,7 +698,7 @@ extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const vo
   if (st) return st;
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_ssm_workspace_bytes(B, L, ds), HDCM_EWORKSPACE);
-  HDCM_CHECK_ARG(((uintptr_t)ws & 3u) == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(((uintptr_t)ws & 255u) == 0, HDCM_EALIGN);
   return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, dtype,
                              (hipStream_t)stream);
 }

@@ -6,10 +6,11 @@
 // library runs on holds its own copy of the array (until the process ends) at its own
 // address.  That address is looked up once per device, on the first call that runs on the
 // device, with the device current (hipGetSymbolAddress), and host code passes only it to the
-// kernels: the array's name is a host-side stand-in, not a device address.  The kernels
-// overwrite every scratch value before they read it (the tile totals, then the carried
-// states), so nothing is cleared between calls.  Calls that overlap on one GPU share its
-// array and race.
+// kernels: the array's name is a host-side stand-in, not a device address.  The array starts
+// at zero when the library is loaded, which is the state the scan's workspace needs before
+// its first call; after that the kernel keeps it consistent itself (its call counter, and
+// tile totals tagged with it), so nothing is cleared between calls.  Calls that overlap on
+// one GPU share its array and race.
 #include <mutex>
 
 #include "hdcm_common.h"

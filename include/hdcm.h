@@ -103,6 +103,11 @@ int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_r
  * (threshold 20) and A = -exp(A_log): h_t = h_{t-1} * exp(dt*A) + dt*b*x,
  * y[b,t,:] = h_t.  h0 [B,ds] fp32 (NULL = zeros); h_final [B,ds] fp32 or NULL.
  * y rows may alias the first ds columns of the `combined` buffer.
+ * One launch; every input row is read once.  ws: hdcm_ssm_workspace_bytes(B, L, ds) bytes,
+ * 256-byte aligned, zero-filled before the first call that uses it and passed again as the
+ * previous call left it (the kernel keeps a call counter in it and never needs it cleared
+ * again; a buffer sized for larger inputs serves smaller ones).  Calls that share a
+ * workspace must not overlap (order them on one stream).
  * Replaces: _ssm_intra_v2 + _ssm_scan_v2 + _ssm_inter_v2 launches and the
  *           y_ssm copy into `combined` (hdcmamba/model.py:345-363, 294-295).
  */

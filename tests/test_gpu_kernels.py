@@ -67,7 +67,8 @@ def test_rowln(dev, dtype, W, affine):
 
 # ----------------------------------------------------------------------------- ssm
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("ds,B,L", [(64, 1, 256), (128, 2, 200), (64, 3, 1000)])
+@pytest.mark.parametrize("ds,B,L", [(64, 1, 256), (128, 2, 200), (64, 3, 1000), (32, 2, 700), (192, 1, 3000),
+                                    (128, 1, 32768)])
 def test_ssm(dev, dtype, ds, B, L):
     _say("ssm", dtype, ds, B, L)
     projs, A_log = ssm_inputs(B, L, ds, dtype)
@@ -78,6 +79,47 @@ def test_ssm(dev, dtype, ds, B, L):
     assert_close(buf[..., :ds], y_ref.to(dtype), dtype, "ssm y")
     assert_close(hf, h_ref, dtype, "ssm h_final")
     assert buf[..., ds:].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_ssm_totals_computed_for_their_owners(dev, dtype, monkeypatch):
+    """With no polling budget a workgroup that finds an earlier tile's total missing computes
+    it itself and publishes it for its owner; the outputs are bit-identical to the default
+    (the same code computes every total), with a start state and the final state."""
+    print("ssm forced fallback", dtype, flush=True)
+    ds, B, L = 128, 2, 32768
+    projs, A_log = ssm_inputs(B, L, ds, dtype)
+    pd, ad = projs.to(dev), A_log.to(dev)
+    h0 = torch.randn(B, ds, generator=torch.Generator().manual_seed(3)).to(dev)
+    outs = []
+    for spin in (None, "0"):
+        if spin is not None:
+            monkeypatch.setenv("HDCM_SSM_SPIN_ROUNDS", spin)
+        y = torch.empty(B, L, ds, device=dev, dtype=dtype)
+        hf = torch.empty(B, ds, device=dev)
+        _ops.ssm(pd, ad, ds, y, h0=h0, h_final=hf)
+        torch.cuda.synchronize()
+        outs.append((y, hf))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
+    y_ref, h_ref = oracle.ssm_sequential(projs, A_log, ds, h0=h0.cpu())
+    assert_close(outs[1][0], y_ref.to(dtype), dtype, "ssm y (fallback)")
+    assert_close(outs[1][1], h_ref, dtype, "ssm h_final (fallback)")
+
+
+def test_ssm_workspace_reused_across_shapes(dev):
+    """One workspace serves calls of different shapes in turn: every call's totals carry that
+    call's tag, so words left by an earlier call of another shape are never taken for its."""
+    dtype = torch.bfloat16
+    for B, L, ds in ((2, 4000, 128), (1, 700, 64), (3, 2500, 192), (2, 4000, 128)):
+        print("ssm reuse", B, L, ds, flush=True)
+        projs, A_log = ssm_inputs(B, L, ds, dtype, seed=B * L + ds)
+        y = torch.empty(B, L, ds, device=dev, dtype=dtype)
+        hf = torch.empty(B, ds, device=dev)
+        _ops.ssm(projs.to(dev), A_log.to(dev), ds, y, h_final=hf)
+        y_ref, h_ref = oracle.ssm_sequential(projs, A_log, ds)
+        assert_close(y, y_ref.to(dtype), dtype, f"ssm y {B},{L},{ds}")
+        assert_close(hf, h_ref, dtype, f"ssm h_final {B},{L},{ds}")
 
 
 def test_ssm_h0_continuation(dev):

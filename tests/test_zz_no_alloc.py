@@ -32,7 +32,7 @@ def test_noalloc_matches_workspace_entry_point(dev, dtype):
         projs, A_log = projs.to(dev), A_log.to(dev)
         y_ref = torch.zeros(B, L, ds + 8, device=dev, dtype=dtype)
         hf_ref = torch.zeros(B, ds, device=dev)
-        ws = torch.empty(lib.hdcm_ssm_workspace_bytes(B, L, ds), dtype=torch.uint8, device=dev)
+        ws = torch.zeros(lib.hdcm_ssm_workspace_bytes(B, L, ds), dtype=torch.uint8, device=dev)  # zero before first use
         assert _call("hdcm_ssm_fwd", projs, A_log, ds, y_ref[..., :ds], hf_ref, ws) == 0
         y = torch.zeros_like(y_ref)
         hf = torch.zeros_like(hf_ref)
