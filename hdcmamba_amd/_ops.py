@@ -30,9 +30,9 @@ _PROTOS = {
                                    c_int, c_void_p]),
     "hdcm_ssm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64]),
     "hdcm_ssm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
-                             c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
+                             c_void_p, c_int64, c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_ssm_fwd_noalloc": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_void_p,
-                                     c_int64, c_int64, c_int64, c_int, c_void_p]),
+                                     c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_ssm_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int]),
     "hdcm_ssm_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                              c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_int64, c_int, c_void_p]),
@@ -48,7 +48,7 @@ _PROTOS = {
     "hdcm_slot_state_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t,
                                     c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_slot_gate_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_float,
-                                   c_void_p, c_size_t, c_void_p, c_int64, c_int64, c_void_p,
+                                   c_void_p, c_size_t, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                    c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_slot_attend_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p,
                                      c_size_t, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
@@ -69,6 +69,10 @@ _PROTOS = {
                               c_int64, c_int, c_void_p]),
     "hdcm_rowln_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
                                     c_int64, c_int64, c_int64, c_float, c_int, c_void_p]),
+    "hdcm_rowln_gemm_stats_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                                          c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                          c_float, c_int, c_void_p]),
+    "hdcm_row_sums_fwd": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int, c_void_p]),
     "hdcm_rowln_bwd_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "hdcm_rowln_bwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                                c_void_p, c_void_p, c_size_t, c_int64, c_int64, c_float, c_int, c_void_p]),
@@ -333,8 +337,26 @@ def _ssm_workspace(device, nbytes):
     return ws
 
 
-def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
-    """Selective scan; writes y [B,L,ds] (may be a column slice of a wider buffer)."""
+def _stats_arg(row_stats, part, rows, nparts):
+    """Pointer to part ``part`` and part stride (in pairs) of the partial row statistics
+    ``row_stats`` ([P, rows, 2] fp32, contiguous: the rows of one part adjacent), or (None, 0)."""
+    if row_stats is None:
+        return None, 0
+    if (row_stats.dtype != torch.float32 or not row_stats.is_contiguous() or row_stats.dim() != 3
+            or row_stats.shape[1] != rows or row_stats.shape[2] != 2 or part + nparts > row_stats.shape[0]):
+        raise ValueError(f"row_stats must be a contiguous fp32 [>= {part + nparts}, {rows}, 2] tensor")
+    return row_stats.data_ptr() + 8 * part * rows, rows
+
+
+def ssm_stats_parts(d_state):
+    """Pairs per row the scan writes into row_stats (one per 64-channel block)."""
+    return -(-d_state // 64)
+
+
+def ssm(projs, A_log, d_state, y, h0=None, h_final=None, row_stats=None, stats_part=0):
+    """Selective scan; writes y [B,L,ds] (may be a column slice of a wider buffer).  With
+    ``row_stats`` ([P, B*L, 2] fp32), the sum and sum of squares of each row's stored values
+    per 64-channel block go to parts stats_part, stats_part + 1, ..."""
     _on_gpu(projs, y)
     B, L, _ = projs.shape
     A_log = _same(A_log, projs, "A_log")
@@ -344,10 +366,11 @@ def ssm(projs, A_log, d_state, y, h0=None, h_final=None):
     ws = _ssm_workspace(projs.device, nbytes)
     if h0 is not None:
         h0 = h0.float().contiguous()
+    sp, srs = _stats_arg(row_stats, stats_part, B * L, ssm_stats_parts(d_state))
     ev = timer.begin("ssm")
     _check("hdcm_ssm_fwd", lib().hdcm_ssm_fwd(
         projs.data_ptr(), prs, A_log.data_ptr(), h0.data_ptr() if h0 is not None else None,
-        y.data_ptr(), yrs, h_final.data_ptr() if h_final is not None else None, ws.data_ptr(), nbytes,
+        y.data_ptr(), yrs, h_final.data_ptr() if h_final is not None else None, sp, srs, ws.data_ptr(), nbytes,
         B, L, d_state, _dtype(projs), _stream(projs)))
     timer.end("ssm", ev)
     return y
@@ -366,7 +389,7 @@ def ssm_noalloc(projs, A_log, d_state, y, h0=None, h_final=None):
             raise RuntimeError(f"ssm_noalloc: {name} must be a contiguous fp32 tensor")
     _check("hdcm_ssm_fwd_noalloc", lib().hdcm_ssm_fwd_noalloc(
         projs.data_ptr(), _rows2d(projs, "projs"), A_log.data_ptr(), h0.data_ptr() if h0 is not None else None,
-        y.data_ptr(), _rows2d(y, "y"), h_final.data_ptr() if h_final is not None else None, B, L, d_state,
+        y.data_ptr(), _rows2d(y, "y"), h_final.data_ptr() if h_final is not None else None, None, 0, B, L, d_state,
         _dtype(projs), _stream(projs)))
     return y
 
@@ -487,18 +510,21 @@ def slot_attend(base, q_col, k_col, v_col, gamma, d_model, num_heads, chunk, phi
 
 
 def slot_gate(projs, q_col, gamma, gn_w, gn_b, gn_eps, ws, out, out_col, d_model, num_heads, chunk,
-              S_final=None):
-    """Slot memory + GroupNorm + sigmoid gate into out[..., out_col:out_col+d_model]."""
+              S_final=None, row_stats=None, stats_part=0):
+    """Slot memory + GroupNorm + sigmoid gate into out[..., out_col:out_col+d_model].  With
+    ``row_stats`` ([P, B*L, 2] fp32), the sum and sum of squares of each row's stored values
+    per head go to parts stats_part .. stats_part + num_heads - 1."""
     _on_gpu(projs, out)
     B, L, _ = projs.shape
     gamma = _same(gamma, projs, "gamma")
     gn_w = _same(gn_w, projs, "gn_w")
     gn_b = _same(gn_b, projs, "gn_b")
+    sp, srs = _stats_arg(row_stats, stats_part, B * L, num_heads)
     ev = timer.begin("slot_gate")
     _check("hdcm_slot_gate_fwd", lib().hdcm_slot_gate_fwd(
         projs.data_ptr(), _rows2d(projs, "projs"), q_col, gamma.data_ptr(), gn_w.data_ptr(),
         gn_b.data_ptr(), float(gn_eps), ws.data_ptr(), ws.numel(), out.data_ptr(), _rows2d(out, "out"),
-        out_col, S_final.data_ptr() if S_final is not None else None, B, L, d_model, num_heads, chunk,
+        out_col, S_final.data_ptr() if S_final is not None else None, sp, srs, B, L, d_model, num_heads, chunk,
         _dtype(projs), _stream(projs)))
     timer.end("slot_gate", ev)
     return out
@@ -669,6 +695,57 @@ def rowln_gemm(c, weight, residual, eps=1e-5, out=None):
         o2.stride(0), M, N, K, float(eps), _dtype(c), _stream(c)))
     timer.end("rowln_gemm", ev)
     return out
+
+
+def row_sums(weight, out=None):
+    """fp32 [N] sums of the rows of a bf16 [N, K] weight (hdcm_row_sums_fwd), into ``out``
+    when given."""
+    _on_gpu(weight)
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    N, K = w.shape
+    sums = torch.empty(N, device=w.device, dtype=torch.float32) if out is None else out
+    if sums.dtype != torch.float32 or not sums.is_contiguous() or sums.numel() != N:
+        raise ValueError(f"row_sums: out must be a contiguous fp32 tensor of {N} values")
+    _check("hdcm_row_sums_fwd", lib().hdcm_row_sums_fwd(w.data_ptr(), w.stride(0), N, K, sums.data_ptr(),
+                                                        _dtype(w), _stream(w)))
+    return sums
+
+
+def rowln_gemm_stats(c, weight, w_sums, row_stats, residual, eps=1e-5, out=None):
+    """rowln_gemm with the row statistics and the weight row sums supplied: ``row_stats``
+    [P, rows, 2] fp32 holds per row P (sum, sum of squares) pairs of disjoint column blocks
+    covering c's last dim (as ssm and slot_gate write them), ``w_sums`` = row_sums(weight).
+    ``out`` may be ``residual``."""
+    _on_gpu(c, weight, residual)
+    K = c.shape[-1]
+    N = weight.shape[0]
+    c2 = _rows_view(c, K)
+    M = c2.shape[0]
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    r2 = residual.reshape(-1, N)
+    if r2.stride(-1) != 1:
+        raise ValueError("residual must have a unit inner stride")
+    sp, stride = _stats_arg(row_stats, 0, M, 1)
+    parts = row_stats.shape[0]
+    if w_sums.dtype != torch.float32 or not w_sums.is_contiguous() or w_sums.numel() != N:
+        raise ValueError(f"w_sums must be a contiguous fp32 tensor of {N} values")
+    if out is None:
+        out = torch.empty(*c.shape[:-1], N, device=c.device, dtype=c.dtype)
+    o2 = out.view(-1, N)
+    ev = timer.begin("rowln_gemm")
+    _check("hdcm_rowln_gemm_stats_fwd", lib().hdcm_rowln_gemm_stats_fwd(
+        c2.data_ptr(), c2.stride(0), w.data_ptr(), w.stride(0), w_sums.data_ptr(), sp, parts, stride, r2.data_ptr(),
+        r2.stride(0), o2.data_ptr(), o2.stride(0), M, N, K, float(eps), _dtype(c), _stream(c)))
+    timer.end("rowln_gemm", ev)
+    return out
+
+
+def rowln_stats_ok(c, N):
+    """Whether rowln_gemm_stats takes c [.., K] with N outputs: bf16, more rows than the decode
+    step kernels handle, and the 16-byte runs it needs (N a multiple of 8)."""
+    K = c.shape[-1]
+    rows = c.numel() // K if K else 0
+    return c.dtype == torch.bfloat16 and rows > SKINNY_MAX_ROWS and N % 8 == 0 and K % 8 == 0
 
 
 def skinny_ok(x: torch.Tensor, weight: torch.Tensor) -> bool:

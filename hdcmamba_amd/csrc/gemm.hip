@@ -4,6 +4,8 @@
 //   EPI_BIAS:   + bias[o]                                  (in_proj: hdcmamba/model.py:313,340)
 //   EPI_ROWLN:  res[t, o] + r_t * (acc - mu_t * s_o)       (out_proj over the row LayerNorm
 //               and the residual add: model.py:382-383,394)
+//   EPI_ROWSTATS: the same value, with mu_t, r_t from row statistics its producers wrote and s
+//               from a cached weight-row-sum vector (see "Row statistics from the producers")
 // The row LayerNorm of out_proj's input (no affine, eps) folds into the epilogue:
 //   LN(c)_t W^T = r_t (c_t - mu_t 1) W^T = r_t (c_t W^T - mu_t s),  s_o = sum_k W[o, k],
 // so the normalized rows never exist in memory.  mu_t, r_t = 1/sqrt(var_t + eps) and s_o
@@ -24,6 +26,17 @@
 // groups (SQ_LDS_BANK_CONFLICT reads 0).  Rows past M or N read as zeros (buffer range
 // checking); K columns past K get an out-of-range offset, also zeros.
 //
+// Row statistics from the producers (EPI_ROWSTATS): the kernels that write the rows of X
+// (the scan and the slot gate) also write, per row, the sum and sum of squares of each
+// 64-column block they stored, as rounded, block-major; s comes from hdcm_row_sums_fwd, computed once per
+// weight.  At its start a workgroup loads its 256 x 256 residual tile (16-byte runs, traded
+// into the accumulator layout with v_permlane16_swap), reduces its 256 rows' partial sums to
+// (mu_t, r_t) and starts the accumulators at res / r_t - mu_t * s_o; the epilogue then writes
+// r_t * acc as 16-byte runs.  The residual's read overlaps the first operand tiles' loads and
+// nothing is read after the K loop.  Measured in isolation at 32768 x 1024 x 1152: 86-90 us
+// against 103-110 us for EPI_ROWLN (whose in-loop v_dot2 sums, reductions and 8-byte
+// epilogue loads and stores make the difference).
+//
 // Workgroup order: workgroup b runs on XCD b % 8 (round-robin dispatch).  XCD x takes a
 // contiguous run of tile indices, walked in bands of kGroup o-tiles (o fastest inside a
 // band), so the ~32 workgroups resident on one XCD share a few W and X panels in its L2.
@@ -41,7 +54,7 @@ constexpr int kBufferFlags = 0x00020000;   // buffer resource word 3: raw 32-bit
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-enum { EPI_BIAS = 0, EPI_ROWLN = 1 };
+enum { EPI_BIAS = 0, EPI_ROWLN = 1, EPI_ROWSTATS = 2 };
 
 __shared__ uint4 sW0[kBO * kChunks], sW1[kBO * kChunks], sX0[kBT * kChunks], sX1[kBT * kChunks];
 
@@ -62,7 +75,8 @@ template <int EPI, bool BIAS>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bt_kernel(
     const bf16_t* __restrict__ X, int64_t x_rs, const bf16_t* __restrict__ W, int64_t w_rs,
     const bf16_t* __restrict__ bias, const bf16_t* res, int64_t r_rs, bf16_t* out,
-    int64_t o_rs, int M, int N, int K, int n_otiles, float eps) {
+    int64_t o_rs, int M, int N, int K, int n_otiles, float eps, const float* __restrict__ wsum,
+    const float* __restrict__ rstats, int nparts, int64_t stats_ps) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   int ot, tt;
@@ -96,11 +110,87 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bt_kernel(
 
   const int wo = w & 1, wt = w >> 1;
   const int l16 = lane & 15, g = lane >> 4;
+  // EPI_ROWSTATS lanes hold 8 consecutive columns for 16-byte runs: for the column tiles 2ip,
+  // 2ip+1 of a row, lane group g takes columns 32 ip + gcol .. +7 (v_permlane16_swap trades
+  // the 4+4 values of the MFMA layout between lanes g and g^1)
+  const int gcol = 16 * (g & 1) + 8 * (g >> 1);
   f32x4_t acc[8][4];
+  float rs[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (EPI == EPI_ROWSTATS) {
+    uint4 rraw[4][4];  // residual, 8 columns per (16-token tile j, column-tile pair ip)
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+    for (int j = 0; j < 4; ++j) {
+      const int t = min(t0 + wt * 64 + j * 16 + l16, M - 1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int ip = 0; ip < 4; ++ip) {
+        const int o = min(o0 + wo * 128 + ip * 32 + gcol, N - 8);
+        rraw[j][ip] = *reinterpret_cast<const uint4*>(res + (int64_t)t * r_rs + o);
+      }
+    }
+    float4 sv[8];  // s_o of the MFMA layout's columns o0 + 128 wo + 16 i + 4 g .. +3
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      sv[i] = *reinterpret_cast<const float4*>(wsum + min(o0 + wo * 128 + i * 16 + 4 * g, N - 4));
+    issue(sW0, sX0, 0);
+    // (mu, r) of the tile's rows.  Thread tid adds the partial sums of row t0 + tid % 256
+    // with parts q = tid / 256, +2, +4, ... (part-major: 256 threads read 256 consecutive
+    // pairs), 16 loads in flight at a time; the two halves meet in LDS.
+    float2* mr = reinterpret_cast<float2*>(sW1);  // stage 1's buffer, loaded only after the loop's first barrier
+    {
+      constexpr int kBatch = 16;
+      const int half = tid / kBT;
+      const float2* ps = reinterpret_cast<const float2*>(rstats) + min(t0 + tid % kBT, M - 1);
+      float s1 = 0.f, s2 = 0.f;
+      for (int q0 = half; q0 < nparts; q0 += 2 * kBatch) {
+        float2 v[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k)
+          v[k] = q0 + 2 * k < nparts ? ps[(int64_t)(q0 + 2 * k) * stats_ps] : make_float2(0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+          s1 += v[k].x;
+          s2 += v[k].y;
+        }
+      }
+      mr[tid] = make_float2(s1, s2);  // [half][row]
+    }
+    __syncthreads();
+    float mu[4];
+    const float invK = 1.0f / (float)K;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wt * 64 + j * 16 + l16;
+      const float2 a = mr[row], b = mr[kBT + row];
+      const float m = (a.x + b.x) * invK;
+      mu[j] = m;
+      rs[j] = rsqrtf(fmaxf((a.y + b.y) * invK - m * m, 0.f) + eps);
+    }
+    // acc = res / r - mu * s, so that r * (acc + c w^T) = res + r (c w^T - mu s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sd = 1.0f / rs[j];
+#pragma unroll
+      for (int ip = 0; ip < 4; ++ip) {
+        const auto s0 = __builtin_amdgcn_permlane16_swap(rraw[j][ip].x, rraw[j][ip].z, false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(rraw[j][ip].y, rraw[j][ip].w, false, false);
+        const uint32_t rw[2][2] = {{s0[0], s1[0]}, {s0[1], s1[1]}};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int i = 2 * ip + h;
+          const float r4[4] = {__uint_as_float(rw[h][0] << 16), __uint_as_float(rw[h][0] & 0xffff0000u),
+                               __uint_as_float(rw[h][1] << 16), __uint_as_float(rw[h][1] & 0xffff0000u)};
+          const float s4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][e] = fmaf(r4[e], sd, -mu[j] * s4[e]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
   // EPI_ROWLN sums, taken in turns so each wave adds on a fraction of the K steps:
   //   ssum/ssq: sum c and sum c^2 of token l16 of the wave's j-th 16-token tile, on the K
   //   steps with kt % 2 == wo (the two waves sharing the tokens alternate);
@@ -169,7 +259,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bt_kernel(
   };
 
   const int nk = (K + kBK - 1) / kBK;
-  issue(sW0, sX0, 0);
+  if constexpr (EPI != EPI_ROWSTATS) issue(sW0, sX0, 0);
   for (int kt = 0; kt < nk; ++kt) {
     const bool odd = kt & 1;
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of tile kt are in LDS
@@ -178,6 +268,28 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bt_kernel(
     compute(odd ? sW1 : sW0, odd ? sX1 : sX0, kt);
   }
 
+  if constexpr (EPI == EPI_ROWSTATS) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = t0 + wt * 64 + j * 16 + l16;
+#pragma unroll
+      for (int ip = 0; ip < 4; ++ip) {
+        uint32_t w2[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const f32x4_t a = acc[2 * ip + h][j];
+          w2[h][0] = pack_bf16x2(rs[j] * a[0], rs[j] * a[1]);
+          w2[h][1] = pack_bf16x2(rs[j] * a[2], rs[j] * a[3]);
+        }
+        const auto s0 = __builtin_amdgcn_permlane16_swap(w2[0][0], w2[1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane16_swap(w2[0][1], w2[1][1], false, false);
+        const int o = o0 + wo * 128 + ip * 32 + gcol;
+        if (t < M && o < N)
+          *reinterpret_cast<uint4*>(out + (int64_t)t * o_rs + o) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+      }
+    }
+    return;
+  }
   uint2 rcur[8], rnext[8];
   auto load_res = [&](int j, uint2 (&r)[8]) {
     const int t = min(t0 + wt * 64 + j * 16 + l16, M - 1);
@@ -189,7 +301,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bt_kernel(
   };
   // the first residual rows are in flight while the statistics are reduced
   if (EPI == EPI_ROWLN) load_res(0, rcur);
-  float mu[4] = {0.f, 0.f, 0.f, 0.f}, rs[4] = {1.f, 1.f, 1.f, 1.f};
+  float mu[4] = {0.f, 0.f, 0.f, 0.f};  // rs (above) stays 1 for EPI_BIAS
   const float* wrow = nullptr;  // EPI_ROWLN: s of this tile's 256 weight rows, in LDS
   if (EPI == EPI_ROWLN) {
     // totals over the four lane groups, then over the waves sharing a row (LDS)
@@ -311,7 +423,8 @@ extern "C" int hdcm_gemm_fwd(const void* x, int64_t x_row_stride, const void* w,
   auto kern = bias ? gemm_bt_kernel<EPI_BIAS, true> : gemm_bt_kernel<EPI_BIAS, false>;
   HDCM_LAUNCH(kern, dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0, (hipStream_t)stream, (const bf16_t*)x,
                      x_row_stride, (const bf16_t*)w, w_row_stride, (const bf16_t*)bias, (const bf16_t*)nullptr,
-                     (int64_t)0, (bf16_t*)out, out_row_stride, (int)M, (int)N, (int)K, (int)n_ot, 0.f);
+                     (int64_t)0, (bf16_t*)out, out_row_stride, (int)M, (int)N, (int)K, (int)n_ot, 0.f,
+                     (const float*)nullptr, (const float*)nullptr, 0, (int64_t)0);
   return hdcm_launch_status();
 }
 
@@ -332,6 +445,64 @@ extern "C" int hdcm_rowln_gemm_fwd(const void* c, int64_t c_row_stride, const vo
   HDCM_LAUNCH((gemm_bt_kernel<EPI_ROWLN, false>), dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0,
                      (hipStream_t)stream, (const bf16_t*)c, c_row_stride, (const bf16_t*)w, w_row_stride,
                      (const bf16_t*)nullptr, (const bf16_t*)res, res_row_stride, (bf16_t*)out, out_row_stride, (int)M,
-                     (int)N, (int)K, (int)n_ot, eps);
+                     (int)N, (int)K, (int)n_ot, eps, (const float*)nullptr, (const float*)nullptr, 0, (int64_t)0);
+  return hdcm_launch_status();
+}
+
+namespace {
+
+// s_o = sum_k W[o, k] in fp32, one wave per weight row.
+__global__ __launch_bounds__(256) void row_sums_kernel(const bf16_t* __restrict__ W, int64_t w_rs, int N, int K,
+                                                       float* __restrict__ sums) {
+  const int o = blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (o >= N) return;
+  const bf16_t* row = W + (int64_t)o * w_rs;
+  float s = 0.f, q = 0.f;
+  for (int k = 8 * lane; k < K; k += 8 * 64) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + k);
+    bf16_pair_sums(v.x, s, q);
+    bf16_pair_sums(v.y, s, q);
+    bf16_pair_sums(v.z, s, q);
+    bf16_pair_sums(v.w, s, q);
+  }
+  s = wave_sum(s);
+  if (lane == 0) sums[o] = s;
+}
+
+}  // namespace
+
+extern "C" int hdcm_row_sums_fwd(const void* w, int64_t w_row_stride, int64_t N, int64_t K, float* sums,
+                                 int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(N >= 0 && K > 0 && w_row_stride >= K && ((w && sums) || N == 0), HDCM_EINVAL);
+  HDCM_CHECK_ARG(K % 8 == 0 && w_row_stride % 8 == 0 && hdcm_aligned16(w) && ((uintptr_t)sums & 3u) == 0,
+                 HDCM_EALIGN);
+  HDCM_CHECK_ARG(N <= ((int64_t)1 << 30), HDCM_EUNSUPPORTED);
+  if (N == 0) return HDCM_OK;
+  HDCM_LAUNCH(row_sums_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, (hipStream_t)stream, (const bf16_t*)w,
+              w_row_stride, (int)N, (int)K, sums);
+  return hdcm_launch_status();
+}
+
+extern "C" int hdcm_rowln_gemm_stats_fwd(const void* c, int64_t c_row_stride, const void* w, int64_t w_row_stride,
+                                         const float* w_sums, const float* row_stats, int64_t stats_parts,
+                                         int64_t stats_part_stride, const void* res, int64_t res_row_stride, void* out, int64_t out_row_stride,
+                                         int64_t M, int64_t N, int64_t K, float eps, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  const int st = check_common(c, c_row_stride, w, w_row_stride, out, out_row_stride, M, N, K);
+  if (st) return st;
+  HDCM_CHECK_ARG(M == 0 || (res && w_sums && row_stats), HDCM_EINVAL);
+  HDCM_CHECK_ARG(M == 0 || res_row_stride >= N, HDCM_EINVAL);
+  HDCM_CHECK_ARG(stats_parts >= 1 && stats_parts <= (1 << 20) && stats_part_stride >= M, HDCM_EINVAL);
+  // 16-byte residual and output runs
+  HDCM_CHECK_ARG(N % 8 == 0 && res_row_stride % 8 == 0 && out_row_stride % 8 == 0 && hdcm_aligned16(res) &&
+                     hdcm_aligned16(out) && hdcm_aligned16(w_sums) && ((uintptr_t)row_stats & 7u) == 0,
+                 HDCM_EALIGN);
+  if (M == 0) return HDCM_OK;
+  const int64_t n_ot = (N + kBO - 1) / kBO, n_tt = (M + kBT - 1) / kBT;
+  HDCM_LAUNCH((gemm_bt_kernel<EPI_ROWSTATS, false>), dim3((unsigned)(n_ot * n_tt)), dim3(kThreads), 0,
+              (hipStream_t)stream, (const bf16_t*)c, c_row_stride, (const bf16_t*)w, w_row_stride,
+              (const bf16_t*)nullptr, (const bf16_t*)res, res_row_stride, (bf16_t*)out, out_row_stride, (int)M,
+              (int)N, (int)K, (int)n_ot, eps, w_sums, row_stats, (int)stats_parts, stats_part_stride);
   return hdcm_launch_status();
 }

@@ -110,6 +110,39 @@ template <> __device__ __forceinline__ void store16<bf16_t>(bf16_t* p, const flo
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// Adds a packed bf16 pair and its squares to s and q (fp32 accumulation of the exact
+// products, v_dot2_f32_bf16).
+__device__ __forceinline__ void bf16_pair_sums(uint32_t w, float& s, float& q) {
+  typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+  const b16x2 p = __builtin_bit_cast(b16x2, w), one = __builtin_bit_cast(b16x2, 0x3f803f80u);
+  s = __builtin_amdgcn_fdot2_f32_bf16(p, one, s, false);
+  q = __builtin_amdgcn_fdot2_f32_bf16(p, p, q, false);
+}
+
+// store16 that also adds the stored values (as rounded to T) and their squares to s and q:
+// the row statistics a later row LayerNorm needs, taken where the values are produced.
+template <typename T> __device__ __forceinline__ void store16_sums(T* p, const float* in, float& s, float& q);
+template <> __device__ __forceinline__ void store16_sums<float>(float* p, const float* in, float& s, float& q) {
+  store16<float>(p, in);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s += in[e];
+    q = fmaf(in[e], in[e], q);
+  }
+}
+template <> __device__ __forceinline__ void store16_sums<bf16_t>(bf16_t* p, const float* in, float& s, float& q) {
+  uint4 v;
+  v.x = pack_bf16x2(in[0], in[1]);
+  v.y = pack_bf16x2(in[2], in[3]);
+  v.z = pack_bf16x2(in[4], in[5]);
+  v.w = pack_bf16x2(in[6], in[7]);
+  *reinterpret_cast<uint4*>(p) = v;
+  bf16_pair_sums(v.x, s, q);
+  bf16_pair_sums(v.y, s, q);
+  bf16_pair_sums(v.z, s, q);
+  bf16_pair_sums(v.w, s, q);
+}
+
 // Raw (unconverted) 16-byte loads, for staging data whose conversion happens later.
 __device__ __forceinline__ uint4 ldg16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -163,11 +196,19 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-// Sum over the four lanes l, l^16, l^32, l^48 (the row groups of an MFMA C/D tile).
+// Sum over the four lanes l, l^16, l^32, l^48 (the row groups of an MFMA C/D tile), on the
+// gfx950 lane-row swaps (VALU, no LDS traffic).  v_permlane16_swap(a, b) returns
+// (a.r0, b.r0, a.r2, b.r2) and (a.r1, b.r1, a.r3, b.r3) for 16-lane rows r0..r3, so with
+// a = b = v their sum is r0+r1 in rows 0-1 and r2+r3 in rows 2-3; v_permlane32_swap returns
+// (a.r0, a.r1, b.r0, b.r1) and (a.r2, a.r3, b.r2, b.r3), whose sum adds the two halves.
+// Every lane gets (x0 + x1) + (x2 + x3), bit for bit.
 __device__ __forceinline__ float quad_group_sum(float v) {
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  const unsigned u = __float_as_uint(v);
+  const auto h = __builtin_amdgcn_permlane16_swap(u, u, true, false);  // fetch inactive lanes too
+  const float s = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const unsigned us = __float_as_uint(s);
+  const auto q = __builtin_amdgcn_permlane32_swap(us, us, true, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // softplus with the threshold 20 of F.softplus: x above it, log(1 + exp(x)) below.

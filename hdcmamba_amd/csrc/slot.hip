@@ -316,7 +316,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     const T* __restrict__ projs, int64_t prs, int q_col, int k_off, int v_off, int g_off, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
     float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
-    int64_t ors, int out_col, float* __restrict__ S_final, const T* __restrict__ zb = nullptr, int64_t zrs = 0) {
+    int64_t ors, int out_col, float* __restrict__ S_final, float* __restrict__ row_stats, int64_t stats_ps,
+    const T* __restrict__ zb = nullptr, int64_t zrs = 0) {
   using LD = Lds<T, HD, TC>;
   using TL = TileLoader<T, HD, TC, 0, 3>;
   static_assert(LD::total * sizeof(T) + 2 * HD * sizeof(float) <= 160 * 1024, "LDS budget");
@@ -531,6 +532,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           return yacc[vt][r];
         }
       };
+      // with row_stats (EPI): the sum and sum of squares of the stored (rounded) values of row
+      // iq over the head's HD columns, the partial statistics of the row LayerNorm after it
+      float st_s = 0.f, st_q = 0.f;
       if constexpr (kPairs) {
         // Tiles vt = 2pp and 2pp+1 leave this lane 4+4 values of row iq; one
         // v_permlane16_swap per packed word trades them between the lane pairs (kg, kg^1) of
@@ -561,6 +565,10 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
             }
             ow[hv][0] = pack_bf16x2(o[0], o[1]);
             ow[hv][1] = pack_bf16x2(o[2], o[3]);
+            if constexpr (EPI) {
+              bf16_pair_sums(ow[hv][0], st_s, st_q);
+              bf16_pair_sums(ow[hv][1], st_s, st_q);
+            }
           }
           const auto s0 = __builtin_amdgcn_permlane16_swap(ow[0][0], ow[1][0], false, false);
           const auto s1 = __builtin_amdgcn_permlane16_swap(ow[0][1], ow[1][1], false, false);
@@ -585,6 +593,14 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
           if constexpr (EPI) load4<T>(reinterpret_cast<const T*>(&graw[vt]), gv);
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = out_val(vt, r, gv[r]);
+          if constexpr (EPI) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float sv = rnd<T>(o[r]);
+              st_s += sv;
+              st_q = fmaf(sv, sv, st_q);
+            }
+          }
           if constexpr (CHAIN) {
             float z[4];
             load4<T>(reinterpret_cast<const T*>(&graw[vt]), z);
@@ -592,6 +608,14 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
             for (int r = 0; r < 4; ++r) o[r] *= z[r] > 0.f ? 1.0f : fexp(z[r]);
           }
           store4<T>(orow + vt * 16, o);
+        }
+      }
+      if constexpr (EPI) {
+        if (row_stats != nullptr) {  // the row's 4 lanes l16 + 16 kg
+          st_s = quad_group_sum(st_s);
+          st_q = quad_group_sum(st_q);
+          if (kg == 0 && iq < tlen)
+            *reinterpret_cast<float2*>(row_stats + 2 * (h * stats_ps + rowbase + p + iq)) = make_float2(st_s, st_q);
         }
       }
       // next tile's gate (this tile's again after the last: a fixed load count)
@@ -855,8 +879,9 @@ int launch_state(const void* base, int64_t prs, int64_t k_col, int64_t v_off, co
 template <typename T, int HD, bool PHI, bool EPI, bool CHAIN = false>
 int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int64_t v_off, int64_t g_off,
                 const void* gamma, const void* gn_w, const void* gn_b, float gn_eps, const void* ws, void* out,
-                int64_t ors, int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t H, int64_t C,
-                const SlotPlan& pl, hipStream_t s, const void* zb = nullptr, int64_t zrs = 0) {
+                int64_t ors, int64_t out_col, float* S_final, float* row_stats, int64_t stats_ps, int64_t B,
+                int64_t L, int64_t H, int64_t C, const SlotPlan& pl, hipStream_t s, const void* zb = nullptr,
+                int64_t zrs = 0) {
   constexpr int TC = TileOf<T>::value;
   const float* Ain = (const float*)ws + (size_t)B * H * pl.nseg * HD * HD;
   // heads vary fastest so the workgroups that run together read the same rows of projs
@@ -869,7 +894,7 @@ int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int
   HDCM_LAUNCH((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
                      (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
                      pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, \
-                     pl.nseg, (T*)out, ors, (int)out_col, S_final, (const T*)zb, zrs)
+                     pl.nseg, (T*)out, ors, (int)out_col, S_final, row_stats, stats_ps, (const T*)zb, zrs)
   if (pl.has_w) {
     if (pairs) HDCM_GATE_LAUNCH(true, true);
     else HDCM_GATE_LAUNCH(true, false);
@@ -934,8 +959,8 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
                                   const void* gamma, const void* gn_w, const void* gn_b,
                                   float gn_eps, const void* ws, size_t ws_bytes, void* out,
                                   int64_t out_row_stride, int64_t out_col, float* S_final,
-                                  int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C,
-                                  int dtype, void* stream) {
+                                  float* row_stats, int64_t stats_part_stride, int64_t B, int64_t L,
+                                  int64_t dm, int64_t H, int64_t C, int dtype, void* stream) {
   SlotPlan pl;
   int st = slot_plan(B, L, dm, H, C, dtype, &pl);
   if (st) return st;
@@ -947,6 +972,9 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
   // Output runs of 4 elements must be naturally aligned (8 bytes bf16, 16 bytes fp32).
   HDCM_CHECK_ARG(((uintptr_t)out % (4 * esz)) == 0 && out_col % 4 == 0 && out_row_stride % 4 == 0,
                  HDCM_EALIGN);
+  // row_stats: one (sum, sum of squares) pair per head and row, head-major
+  HDCM_CHECK_ARG(!row_stats || stats_part_stride >= B * L, HDCM_EINVAL);
+  HDCM_CHECK_ARG(((uintptr_t)row_stats & 7u) == 0, HDCM_EALIGN);
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= slot_ws_bytes(B, H, pl), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
@@ -954,8 +982,8 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
 #define HDCM_GATE_CASE(TT, HDV)                                                                 \
   if (pl.HD == HDV)                                                                            \
     return launch_gate<TT, HDV, true, true>(projs, proj_row_stride, q_col, dm, 2 * dm, 3 * dm, gamma, gn_w,  \
-                                            gn_b, gn_eps, ws, out, out_row_stride, out_col, S_final, B, L, H, \
-                                            C, pl, s);
+                                            gn_b, gn_eps, ws, out, out_row_stride, out_col, S_final, row_stats, \
+                                            stats_part_stride, B, L, H, C, pl, s);
   if (dtype == HDCM_BF16) {
     HDCM_GATE_CASE(bf16_t, 32)
     HDCM_GATE_CASE(bf16_t, 64)
@@ -1006,11 +1034,11 @@ extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_
     if (chain)                                                                                               \
       return launch_gate<TT, HDV, PH, false, true>(base, row_stride, q_col, k_col - q_col, v_col - q_col, 0,  \
                                                    gamma, nullptr, nullptr, 0.f, ws, out, out_row_stride,    \
-                                                   out_col, nullptr, B, L, H, C, pl, s, chain,               \
+                                                   out_col, nullptr, nullptr, 0, B, L, H, C, pl, s, chain,   \
                                                    chain_row_stride);                                        \
     return launch_gate<TT, HDV, PH, false>(base, row_stride, q_col, k_col - q_col, v_col - q_col, 0, gamma,   \
                                            nullptr, nullptr, 0.f, ws, out, out_row_stride, out_col, nullptr, \
-                                           B, L, H, C, pl, s);                                              \
+                                           nullptr, 0, B, L, H, C, pl, s);                                  \
   }
   if (dtype == HDCM_BF16) {
     HDCM_ATTEND_CASE(bf16_t, 32, true)

@@ -10,7 +10,7 @@
 //   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2).
 //
 // Forward (ssm_scan_kernel): one launch that reads every input once.  A workgroup owns a
-// tile of TR rows x 64 channels.  A thread holds 8 consecutive rows x one 16-byte channel
+// tile of TR rows x 64 channels.  A thread holds 4 consecutive rows x one 16-byte channel
 // group, scans them serially in registers, and the row groups are combined by a lane scan
 // (shuffles) and across waves through LDS.  The workgroup then publishes its tile total
 // (A, H) per channel and folds the totals of all earlier tiles of its sequence into the
@@ -23,7 +23,10 @@
 // (it must be zero before its first use).  A workgroup that finds an earlier total missing
 // polls for a bounded number of rounds, then computes that tile's total itself with the
 // same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
-// whatever order the workgroups run in.
+// whatever order the workgroups run in.  With row_stats the workgroup also writes, per row,
+// the sum and the sum of squares of the 64 values it stored (as rounded), block-major (the
+// rows of one channel block contiguous): the partial statistics of the row LayerNorm that
+// follows, taken without another read of y.
 //
 // Backward (the adjoint scan, reversed rows): the three-pass form below.
 //   1. ssm_tile_kernel<SUMMARY>: stage a tile's (a, u) pairs for 64 channels through LDS,
@@ -464,8 +467,9 @@ __device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int
 template <typename T>
 __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     const T* __restrict__ projs, int64_t prs, const T* __restrict__ A_log, const float* __restrict__ h0,
-    T* __restrict__ y, int64_t yrs, float* __restrict__ h_final, unsigned* __restrict__ hdr,
-    unsigned long long* __restrict__ words, int words_bytes, int L, int ds, int ntiles, int spin_rounds) {
+    T* __restrict__ y, int64_t yrs, float* __restrict__ h_final, float* __restrict__ row_stats, int64_t stats_ps,
+    unsigned* __restrict__ hdr, unsigned long long* __restrict__ words, int words_bytes, int L, int ds, int ntiles,
+    int spin_rounds) {
   using S = ScanShape<T>;
   constexpr int E = S::E, CG = S::CG;
   constexpr int CPW = kScanCh / kScanWaves;  // look-back channels per wave
@@ -602,20 +606,34 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   float hs[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) hs[e] = fmaf(xa[e], s_hin[cg * E + e], xh[e]);
+  float rsum[kRPT], rsq[kRPT];  // this thread's part of each row's sum and sum of squares
   if (cok) {
     T* yb = y + rowbase * yrs + c0 + cg * E;
 #pragma unroll
     for (int r = 0; r < kRPT; ++r) {
       const int t = r0 + r;
-      if (t >= L) break;
+      rsum[r] = rsq[r] = 0.f;
+      if (t >= L) continue;
       float v[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) v[e] = fmaf(At[r][e], hs[e], Ut[r][e]);
-      store16<T>(yb + (int64_t)t * yrs, v);
+      store16_sums<T>(yb + (int64_t)t * yrs, v, rsum[r], rsq[r]);
       if (h_final != nullptr && t == L - 1) {
 #pragma unroll
         for (int e = 0; e < E; ++e) h_final[(int64_t)b * ds + c0 + cg * E + e] = v[e];
       }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) rsum[r] = rsq[r] = 0.f;
+  }
+  if (row_stats != nullptr) {  // the CG threads of a row group are consecutive lanes
+#pragma unroll
+    for (int r = 0; r < kRPT; ++r) {
+      const float s = group_sum<CG>(rsum[r]), q = group_sum<CG>(rsq[r]);
+      const int t = r0 + r;
+      if (cg == 0 && t < L)
+        *reinterpret_cast<float2*>(row_stats + 2 * (chb * stats_ps + rowbase + t)) = make_float2(s, q);
     }
   }
 
@@ -641,14 +659,15 @@ int spin_rounds_setting() {
 
 template <typename T>
 int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, void* y,
-           int64_t yrs, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds,
-           hipStream_t s) {
+           int64_t yrs, float* h_final, float* row_stats, int64_t stats_ps, void* ws, int64_t B, int64_t L,
+           int64_t ds, hipStream_t s) {
   const int64_t nt = (L + ScanShape<T>::TR - 1) / ScanShape<T>::TR;
   const dim3 grid((unsigned)nt, (unsigned)((ds + kScanCh - 1) / kScanCh), (unsigned)B);
   const ScanWorkspace w = scan_workspace(B, L, ds);
   char* base = (char*)ws;
   HDCM_LAUNCH((ssm_scan_kernel<T>), grid, dim3(kScanThreads), 0, s, (const T*)projs, prs, (const T*)A_log, h0, (T*)y,
-              yrs, h_final, (unsigned*)base, (unsigned long long*)(base + w.words_at), (int)w.words_bytes, (int)L,
+              yrs, h_final, row_stats, stats_ps, (unsigned*)base, (unsigned long long*)(base + w.words_at),
+              (int)w.words_bytes, (int)L,
               (int)ds, (int)nt, spin_rounds_setting());
   return hdcm_launch_status();
 }
@@ -664,7 +683,8 @@ extern "C" size_t hdcm_ssm_workspace_bytes(int64_t B, int64_t L, int64_t ds) {
 // Argument checks of the forward entry points, everything but the workspace (also used by
 // other sources of the library that run these kernels).
 int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const void* y,
-                       int64_t y_row_stride, int64_t B, int64_t L, int64_t ds, int dtype) {
+                       int64_t y_row_stride, const float* row_stats, int64_t stats_part_stride, int64_t B,
+                       int64_t L, int64_t ds, int dtype) {
   HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(A_log && ((projs && y) || B == 0 || L == 0), HDCM_EINVAL);  // empty: NULL data allowed
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && ds > 0, HDCM_EINVAL);
@@ -673,6 +693,9 @@ int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A
   HDCM_CHECK_ARG(ds % E == 0 && proj_row_stride % E == 0 && y_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(hdcm_aligned16(projs) && hdcm_aligned16(y) && hdcm_aligned16(A_log), HDCM_EALIGN);
   HDCM_CHECK_ARG(B <= 65535 && ds <= 65535 && L < ((int64_t)1 << 30), HDCM_EUNSUPPORTED);
+  // row_stats: one (sum, sum of squares) pair per 64-channel block and row, block-major
+  HDCM_CHECK_ARG(!row_stats || stats_part_stride >= B * L, HDCM_EINVAL);
+  HDCM_CHECK_ARG(((uintptr_t)row_stats & 7u) == 0, HDCM_EALIGN);
   // the scan kernel counts its workgroups, and addresses its tile totals, in 32 bits
   HDCM_CHECK_ARG(B * ((ds + kScanCh - 1) / kScanCh) * scan_tiles_max(L) < ((int64_t)1 << 31) / (kScanCh * 16),
                  HDCM_EUNSUPPORTED);
@@ -683,24 +706,27 @@ int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A
 // hdcm_ssm_workspace_bytes(B, L, ds) bytes at `ws` (256-byte aligned, zero before its first
 // use, then left as the previous call left it).
 int hdcm_ssm_launch_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const float* h0, void* y,
-                        int64_t y_row_stride, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds, int dtype,
-                        hipStream_t s) {
+                        int64_t y_row_stride, float* h_final, float* row_stats, int64_t stats_part_stride, void* ws,
+                        int64_t B, int64_t L, int64_t ds, int dtype, hipStream_t s) {
   if (dtype == HDCM_F32)
-    return launch<float>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, s);
-  return launch<bf16_t>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, s);
+    return launch<float>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, row_stats, stats_part_stride,
+                         ws, B, L, ds, s);
+  return launch<bf16_t>(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, row_stats, stats_part_stride,
+                        ws, B, L, ds, s);
 }
 
 extern "C" int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
                             const float* h0, void* y, int64_t y_row_stride, float* h_final,
-                            void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds, int dtype,
-                            void* stream) {
-  const int st = hdcm_ssm_check_fwd(projs, proj_row_stride, A_log, y, y_row_stride, B, L, ds, dtype);
+                            float* row_stats, int64_t stats_part_stride, void* ws, size_t ws_bytes, int64_t B,
+                            int64_t L, int64_t ds, int dtype, void* stream) {
+  const int st = hdcm_ssm_check_fwd(projs, proj_row_stride, A_log, y, y_row_stride, row_stats, stats_part_stride, B,
+                                    L, ds, dtype);
   if (st) return st;
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_ssm_workspace_bytes(B, L, ds), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 255u) == 0, HDCM_EALIGN);
-  return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, dtype,
-                             (hipStream_t)stream);
+  return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, row_stats,
+                             stats_part_stride, ws, B, L, ds, dtype, (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------- backward

@@ -19,10 +19,11 @@ static __device__ __align__(256) unsigned char scratch[HDCM_SSM_NOALLOC_SCRATCH_
 
 // ssm.hip
 int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const void* y,
-                       int64_t y_row_stride, int64_t B, int64_t L, int64_t ds, int dtype);
+                       int64_t y_row_stride, const float* row_stats, int64_t stats_part_stride, int64_t B,
+                       int64_t L, int64_t ds, int dtype);
 int hdcm_ssm_launch_fwd(const void* projs, int64_t proj_row_stride, const void* A_log, const float* h0, void* y,
-                        int64_t y_row_stride, float* h_final, void* ws, int64_t B, int64_t L, int64_t ds, int dtype,
-                        hipStream_t s);
+                        int64_t y_row_stride, float* h_final, float* row_stats, int64_t stats_part_stride, void* ws,
+                        int64_t B, int64_t L, int64_t ds, int dtype, hipStream_t s);
 
 namespace {
 
@@ -55,8 +56,10 @@ int scratch_for_stream(hipStream_t s, void** out) {
 
 extern "C" int hdcm_ssm_fwd_noalloc(const void* projs, int64_t proj_row_stride, const void* A_log,
                                     const float* h0, void* y, int64_t y_row_stride, float* h_final,
-                                    int64_t B, int64_t L, int64_t ds, int dtype, void* stream) {
-  int st = hdcm_ssm_check_fwd(projs, proj_row_stride, A_log, y, y_row_stride, B, L, ds, dtype);
+                                    float* row_stats, int64_t stats_part_stride, int64_t B, int64_t L, int64_t ds,
+                                    int dtype, void* stream) {
+  int st = hdcm_ssm_check_fwd(projs, proj_row_stride, A_log, y, y_row_stride, row_stats, stats_part_stride, B, L, ds,
+                              dtype);
   if (st) return st;
   if (B == 0 || L == 0) return HDCM_OK;
   HDCM_CHECK_ARG(hdcm_ssm_workspace_bytes(B, L, ds) <= HDCM_SSM_NOALLOC_SCRATCH_BYTES, HDCM_ETOOBIG);
@@ -64,5 +67,6 @@ extern "C" int hdcm_ssm_fwd_noalloc(const void* projs, int64_t proj_row_stride, 
   void* ws = nullptr;
   st = scratch_for_stream(s, &ws);
   if (st) return st;
-  return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, ws, B, L, ds, dtype, s);
+  return hdcm_ssm_launch_fwd(projs, proj_row_stride, A_log, h0, y, y_row_stride, h_final, row_stats,
+                             stats_part_stride, ws, B, L, ds, dtype, s);
 }

@@ -159,8 +159,10 @@ class ForwardGraph:
     A replay submits the recorded sequence at once, including the side-stream fork and
     join of every block.  ``forward(input_ids)`` copies the ids into the static input
     buffer and returns the static logits buffer, which the next replay overwrites.  The
-    weights are read at replay time (in place updates are seen); the recorded shapes,
-    dtypes and buffers are fixed.
+    weights are read at replay time (in place updates are seen: values derived from a
+    weight and kept between forwards, the out_proj row sums, are refreshed in place before
+    a replay when the weight's version changed); the recorded shapes, dtypes and buffers
+    are fixed.
     """
 
     def __init__(self, lm, input_ids, warmup=2):
@@ -181,11 +183,15 @@ class ForwardGraph:
         self.graph = torch.cuda.CUDAGraph()
         with torch.no_grad(), torch.cuda.graph(self.graph):
             self.logits = lm(self.ids)
+        self._refresh = [m for m in lm.modules() if hasattr(m, "refresh_derived_weights")]
 
     def forward(self, input_ids):
         if input_ids.shape != self.ids.shape:
             raise RuntimeError(f"ForwardGraph was recorded for ids of shape {tuple(self.ids.shape)}, "
                                f"got {tuple(input_ids.shape)}")
+        with torch.no_grad():
+            for m in self._refresh:
+                m.refresh_derived_weights()
         self.ids.copy_(input_ids)
         self.graph.replay()
         return self.logits

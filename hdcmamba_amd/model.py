@@ -214,10 +214,12 @@ class HdcMamba9v3Block(nn.Module):
         self.group_norm = nn.GroupNorm(num_heads, d_model)
         self.register_buffer("gamma_buf", torch.exp(-F.softplus(self.decay_log)))
 
-    def _mixer(self, x, state=None, normalize=True):
+    def _mixer(self, x, state=None, normalize=True, row_stats=None):
         """LN+conv, in_proj, SSM and slot+gate into one `combined` row buffer, then (with
         ``normalize``) its LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm].
-        With ``state``, the SSM and slot states after the last row are written into it."""
+        With ``state``, the SSM and slot states after the last row are written into it.  With
+        ``row_stats`` ([P, B*L, 2] fp32) the SSM and the gate also write each row's partial
+        (sum, sum of squares): the SSM's 64-channel blocks first, then one part per head."""
         B, L, dm = x.shape
         ds, H, C = self.d_state, self.num_heads, self.chunk_size
         dtype = x.dtype
@@ -234,14 +236,16 @@ class HdcMamba9v3Block(nn.Module):
         side = _ops.side_stream(x.device)
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h)
+            _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h,
+                     row_stats=row_stats, stats_part=0)
         gamma = self.gamma_buf.to(dtype)
         q_col = 3 * ds
         ws = _ops.slot_workspace(projs, dm, H, C)
         _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
         main.wait_stream(side)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
-                       combined, ds, dm, H, C, S_final=None if state is None else state.S_prev)
+                       combined, ds, dm, H, C, S_final=None if state is None else state.S_prev,
+                       row_stats=row_stats, stats_part=_ops.ssm_stats_parts(ds))
         if normalize:
             _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
@@ -258,6 +262,50 @@ class HdcMamba9v3Block(nn.Module):
         rows = x.numel() // self.d_model
         tiles = -(-rows // 256) * -(-self.d_model // 256)
         return rows <= 16 or tiles <= 1024
+
+    def _out_weight_sums(self, w):
+        """Row sums of the out_proj weight as used (``w``, the activation-dtype weight), kept
+        until the parameter changes (its storage or its version counter).  A refresh writes
+        into the same buffer, so a recorded graph that reads it sees the new sums."""
+        p = self.out_proj.weight
+        key = (p.data_ptr(), p._version, w.dtype, w.device)
+        if getattr(self, "_wsum_key", None) != key:
+            old = getattr(self, "_wsum", None)
+            if old is not None and old.device == w.device and old.numel() == w.shape[0]:
+                _ops.row_sums(w, out=old)
+            else:
+                self._wsum = _ops.row_sums(w)
+            self._wsum_key = key
+        return self._wsum
+
+    def refresh_derived_weights(self):
+        """Bring the kept out_proj row sums up to date with the weight (a recorded forward
+        graph calls this before each replay; it launches nothing when the weight is
+        unchanged)."""
+        if getattr(self, "_wsum_key", None) is None:
+            return
+        p = self.out_proj.weight
+        if (p.data_ptr(), p._version) != self._wsum_key[:2]:
+            self._out_weight_sums(p.to(self._wsum_key[2]))
+
+    def _fused_mixer_out(self, x, state, out=None):
+        """x + out_proj(LN(combined)) for the fused path, x [B,L,dm]; into ``out`` (which may be
+        x) when given.  With more rows than a decode step the SSM and gate kernels hand the
+        row statistics to the GEMM (hdcm_rowln_gemm_stats_fwd); otherwise the GEMM takes them
+        from its operands (hdcm_rowln_gemm_fwd)."""
+        B, L, dm = x.shape
+        w = self.out_proj.weight.to(x.dtype)
+        x2 = x.reshape(B * L, dm)
+        o2 = None if out is None else out.view(B * L, dm)
+        if _ops.rowln_stats_ok(x2, dm):
+            parts = _ops.ssm_stats_parts(self.d_state) + self.num_heads
+            stats = torch.empty(parts, B * L, 2, device=x.device, dtype=torch.float32)
+            c = self._mixer(x, state, normalize=False, row_stats=stats)
+            y = _ops.rowln_gemm_stats(c, w, self._out_weight_sums(w), stats, x2, out=o2)
+        else:
+            c = self._mixer(x, state, normalize=False)
+            y = _ops.rowln_gemm(c, w, x2, out=o2)
+        return y.view(B, L, dm)
 
     def _differentiable_mixer(self, x):
         """_mixer with autograd through every stage (differentiable_mixer)."""
@@ -277,8 +325,7 @@ class HdcMamba9v3Block(nn.Module):
         """Block body on a chunk-aligned [B,L,dm] input; returns x + out_proj(LN(combined))."""
         B, L, dm = x.shape
         if self._fused_out(x):
-            c = self._mixer(x, state, normalize=False)
-            return _ops.rowln_gemm(c, self.out_proj.weight.to(x.dtype), x.reshape(B * L, dm)).view(B, L, dm)
+            return self._fused_mixer_out(x, state)
         if self.differentiable_mixer and state is None and torch.is_grad_enabled():
             c = self._differentiable_mixer(x)
         else:
@@ -293,9 +340,7 @@ class HdcMamba9v3Block(nn.Module):
         if state is not None:
             self._capture_conv(r, state)
         if self._fused_out(r):
-            c = self._mixer(r, state, normalize=False)
-            r2 = r.view(B * L, dm)
-            _ops.rowln_gemm(c, self.out_proj.weight.to(r.dtype), r2, out=r2)
+            self._fused_mixer_out(r, state, out=r)
             return r
         c = self._mixer(r, state)
         r.view(B * L, dm).addmm_(c, self.out_proj.weight.to(r.dtype).t())

@@ -103,6 +103,10 @@ int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_r
  * (threshold 20) and A = -exp(A_log): h_t = h_{t-1} * exp(dt*A) + dt*b*x,
  * y[b,t,:] = h_t.  h0 [B,ds] fp32 (NULL = zeros); h_final [B,ds] fp32 or NULL.
  * y rows may alias the first ds columns of the `combined` buffer.
+ * row_stats (fp32, or NULL): for row r = b*L+t and 64-channel block c, the pair
+ * (sum, sum of squares) of the y values stored in that block (as rounded) is written to
+ * row_stats[2*(c*stats_part_stride + r)] and the next float; stats_part_stride (in pairs)
+ * >= B*L.  These are partial statistics for hdcm_rowln_gemm_stats_fwd.
  * One launch; every input row is read once.  ws: hdcm_ssm_workspace_bytes(B, L, ds) bytes,
  * 256-byte aligned, zero-filled before the first call that uses it and passed again as the
  * previous call left it (the kernel keeps a call counter in it and never needs it cleared
@@ -114,8 +118,8 @@ int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_r
 size_t hdcm_ssm_workspace_bytes(int64_t B, int64_t L, int64_t ds);
 int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
                  const float* h0, void* y, int64_t y_row_stride, float* h_final,
-                 void* ws, size_t ws_bytes, int64_t B, int64_t L, int64_t ds,
-                 int dtype, void* stream);
+                 float* row_stats, int64_t stats_part_stride, void* ws, size_t ws_bytes,
+                 int64_t B, int64_t L, int64_t ds, int dtype, void* stream);
 
 /*
  * hdcm_ssm_fwd without a workspace argument: the same kernels and results, with their
@@ -131,7 +135,8 @@ int hdcm_ssm_fwd(const void* projs, int64_t proj_row_stride, const void* A_log,
 #define HDCM_SSM_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
 int hdcm_ssm_fwd_noalloc(const void* projs, int64_t proj_row_stride, const void* A_log,
                          const float* h0, void* y, int64_t y_row_stride, float* h_final,
-                         int64_t B, int64_t L, int64_t ds, int dtype, void* stream);
+                         float* row_stats, int64_t stats_part_stride, int64_t B, int64_t L,
+                         int64_t ds, int dtype, void* stream);
 
 /*
  * Gradient of hdcm_ssm_fwd from a zero start state: given gy (the gradient of y) and h (the
@@ -161,7 +166,10 @@ int hdcm_ssm_bwd(const void* projs, int64_t proj_row_stride, const void* A_log, 
  * hdcm_slot_gate_fwd then produces, per (token, head), GroupNorm over hd
  * (gn_eps, affine gn_w/gn_b [dm]) times sigmoid(gate), written to columns
  * [out_col, out_col+dm) of `out`; S_final [B,H,hd,hd] fp32 (or NULL) receives
- * the state after row L-1 (L must then be a multiple of C).
+ * the state after row L-1 (L must then be a multiple of C).  row_stats (fp32, or
+ * NULL): for row r = b*L+t and head h, the pair (sum, sum of squares) of the hd values
+ * stored (as rounded) at row_stats[2*(h*stats_part_stride + r)] and the next float;
+ * stats_part_stride (in pairs) >= B*L (partial statistics for hdcm_rowln_gemm_stats_fwd).
  * Needs hd in {32,64,96,128}; C a power of two dividing the row tile (64 rows
  * for bf16, 32 for fp32) or a multiple of it; L a multiple of C.
  * Replaces: _slot_all_fused launch (hdcmamba/model.py:366-371, kernel
@@ -177,8 +185,9 @@ int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, int64_t q_co
 int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, int64_t q_col,
                        const void* gamma, const void* gn_w, const void* gn_b, float gn_eps,
                        const void* ws, size_t ws_bytes, void* out, int64_t out_row_stride,
-                       int64_t out_col, float* S_final, int64_t B, int64_t L, int64_t dm,
-                       int64_t H, int64_t C, int dtype, void* stream);
+                       int64_t out_col, float* S_final, float* row_stats, int64_t stats_part_stride,
+                       int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype,
+                       void* stream);
 
 /*
  * The slot recurrence without the GroupNorm and gate, on any three column blocks of one
@@ -306,6 +315,30 @@ int hdcm_gemm_fwd(const void* x, int64_t x_row_stride, const void* w, int64_t w_
 int hdcm_rowln_gemm_fwd(const void* c, int64_t c_row_stride, const void* w, int64_t w_row_stride,
                         const void* res, int64_t res_row_stride, void* out, int64_t out_row_stride,
                         int64_t M, int64_t N, int64_t K, float eps, int dtype, void* stream);
+
+/*
+ * hdcm_rowln_gemm_fwd with mu, r and s supplied instead of computed: row_stats holds, per
+ * row t of c, stats_parts pairs (sum, sum of squares) of disjoint column blocks that cover
+ * the K columns, pair p of row t at row_stats[2*(p*stats_part_stride + t)] (as
+ * hdcm_ssm_fwd and hdcm_slot_gate_fwd write them when given the same buffer), summed in
+ * order of p; w_sums [N] fp32 = hdcm_row_sums_fwd of w.  Same result up to
+ * fp32 summation order.  Needs N, res_row_stride and out_row_stride multiples of 8 and res,
+ * out and w_sums 16-byte aligned.  res may alias out.  Replaces, like hdcm_rowln_gemm_fwd,
+ * F.layer_norm(combined.float(), (ds+dm,)).to(dtype), out_proj and the residual add
+ * (hdcmamba/model.py:382-383,394).
+ */
+int hdcm_rowln_gemm_stats_fwd(const void* c, int64_t c_row_stride, const void* w, int64_t w_row_stride,
+                              const float* w_sums, const float* row_stats, int64_t stats_parts,
+                              int64_t stats_part_stride, const void* res, int64_t res_row_stride, void* out, int64_t out_row_stride,
+                              int64_t M, int64_t N, int64_t K, float eps, int dtype, void* stream);
+
+/*
+ * sums[o] = sum_k w[o, k] in fp32 over the K columns of each of N bf16 rows: the weight
+ * row sums hdcm_rowln_gemm_stats_fwd takes (computed once per weight).  No reference
+ * counterpart; part of the out_proj fold above.
+ */
+int hdcm_row_sums_fwd(const void* w, int64_t w_row_stride, int64_t N, int64_t K, float* sums, int dtype,
+                      void* stream);
 
 /*
  * Row LayerNorm over `width` columns, fp32 statistics, optional affine

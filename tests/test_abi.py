@@ -48,6 +48,8 @@ def test_workspace_sizes():
 
 P16 = ctypes.c_void_p(16 * 1024)       # aligned non-null stand-ins: never dereferenced,
 P17 = ctypes.c_void_p(16 * 1024 + 2)   # every call below fails validation first
+P20 = ctypes.c_void_p(16 * 1024 + 4)   # 4-byte aligned only
+P24 = ctypes.c_void_p(16 * 1024 + 8)   # 8-byte aligned only
 
 
 def test_norm_conv_validation():
@@ -67,14 +69,19 @@ def test_norm_conv_validation():
 
 def test_ssm_validation():
     f = _ops.lib().hdcm_ssm_fwd
-    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, P16, 1 << 20, 1, 256, 64, 1, None]
-    a = list(base); a[7] = None
+    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, None, 0, P16, 1 << 20, 1, 256, 64, 1, None]
+    a = list(base); a[9] = None
     assert f(*a) == EWORKSPACE
-    a = list(base); a[8] = 16
+    a = list(base); a[10] = 16
     assert f(*a) == EWORKSPACE
     a = list(base); a[1] = 100
     assert f(*a) == EINVAL
     a = list(base); a[0] = P17
+    assert f(*a) == EALIGN
+    # row statistics: a part stride of at least B*L pairs, 8-byte aligned
+    a = list(base); a[7], a[8] = P16, 255
+    assert f(*a) == EINVAL
+    a = list(base); a[7], a[8] = P20, 256
     assert f(*a) == EALIGN
 
 
@@ -82,14 +89,14 @@ def test_ssm_noalloc_validation():
     """The no-allocation scan checks like hdcm_ssm_fwd and rejects inputs whose scratch would
     exceed its fixed array before any HIP call."""
     f = _ops.lib().hdcm_ssm_fwd_noalloc
-    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, 1, 256, 64, 1, None]
+    base = [P16, 3 * 64 + 8, P16, None, P16, 64, None, None, 0, 1, 256, 64, 1, None]
     a = list(base); a[1] = 100
     assert f(*a) == EINVAL
     a = list(base); a[0] = P17
     assert f(*a) == EALIGN
-    a = list(base); a[7] = 0
+    a = list(base); a[9] = 0
     assert f(*a) == OK  # empty: nothing to do
-    a = list(base); a[7], a[8], a[9] = 64, 32768, 128  # 48 MiB of scratch
+    a = list(base); a[9], a[10], a[11] = 64, 32768, 128  # 48 MiB of scratch
     a[1], a[5] = 3 * 128, 128
     assert f(*a) == ETOOBIG
     assert b"scratch" in _ops.lib().hdcm_strerror(ETOOBIG)
@@ -111,11 +118,15 @@ def test_slot_validation():
     assert st(*a) == EINVAL
     g = lib.hdcm_slot_gate_fwd
     gb = [P16, 3 * 64 + 4 * 256, 3 * 64, P16, P16, P16, 1e-5, P16, 1 << 24, P16, 64 + 256, 64, None,
-          1, 256, 256, 4, 64, 1, None]
+          None, 0, 1, 256, 256, 4, 64, 1, None]
     a = list(gb); a[11] = 62  # output runs of 4 must stay aligned
     assert g(*a) == EALIGN
     a = list(gb); a[10] = 200  # output row too short
     assert g(*a) == EINVAL
+    a = list(gb); a[13], a[14] = P16, 255  # row statistics need a part stride of B*L pairs
+    assert g(*a) == EINVAL
+    a = list(gb); a[13], a[14] = P20, 256
+    assert g(*a) == EALIGN
 
 
 def test_decode_step_validation():
@@ -203,6 +214,32 @@ def test_gemm_validation():
     assert h(*a) == EUNSUPPORTED
     a = list(base); a[8] = 0; a[0] = a[4] = a[6] = None
     assert h(*a) == OK
+    # hdcm_rowln_gemm_stats_fwd(c, c_rs, w, w_rs, w_sums, row_stats, parts, part_stride, res, r_rs, out,
+    #                           o_rs, M, N, K, eps, dtype, stream)
+    g = _ops.lib().hdcm_rowln_gemm_stats_fwd
+    base = [P16, 1152, P16, 1152, P16, P16, 18, 300, P16, 1024, P16, 1024, 300, 1024, 1152, 1e-5, 1, None]
+    a = list(base); a[5] = None  # no row statistics
+    assert g(*a) == EINVAL
+    a = list(base); a[4] = None  # no weight sums
+    assert g(*a) == EINVAL
+    a = list(base); a[6] = 0
+    assert g(*a) == EINVAL
+    a = list(base); a[7] = 299  # part stride shorter than the rows
+    assert g(*a) == EINVAL
+    a = list(base); a[13] = 1020; a[9] = a[11] = 1020  # 16-byte output runs need N % 8 == 0
+    assert g(*a) == EALIGN
+    a = list(base); a[8] = P24  # residual not 16-byte aligned
+    assert g(*a) == EALIGN
+    a = list(base); a[16] = 0
+    assert g(*a) == EUNSUPPORTED
+    a = list(base); a[12] = 0; a[0] = a[8] = a[10] = None
+    assert g(*a) == OK
+    # hdcm_row_sums_fwd(w, w_rs, N, K, sums, dtype, stream)
+    r = _ops.lib().hdcm_row_sums_fwd
+    assert r(P16, 1152, 1024, 1152, None, 1, None) == EINVAL
+    assert r(P16, 1152, 1024, 1150, P16, 1, None) == EALIGN
+    assert r(P16, 1152, 1024, 1152, P16, 0, None) == EUNSUPPORTED
+    assert r(None, 1152, 0, 1152, None, 1, None) == OK
 
 
 def test_norm_conv_bwd_validation():

@@ -373,6 +373,94 @@ def test_rowln_gemm(dev, M, N, K, mean):
     assert torch.equal(rd.cpu(), out.cpu())
 
 
+def _block_sums(vals, width):
+    """[rows, cols] -> [rows, ceil(cols / width), 2] fp64 (sum, sum of squares) per column block."""
+    v = vals.double()
+    nb = -(-v.shape[1] // width)
+    out = torch.zeros(v.shape[0], nb, 2, dtype=torch.float64)
+    for i in range(nb):
+        blk = v[:, i * width:(i + 1) * width]
+        out[:, i, 0] = blk.sum(1)
+        out[:, i, 1] = (blk * blk).sum(1)
+    return out
+
+
+def _check_stats(got, ref, what):
+    torch.cuda.synchronize()
+    g = got.double().cpu()
+    tol = 1e-5 * ref.abs() + 1e-4
+    bad = (g - ref).abs() > tol
+    assert not bad.any(), f"{what}: {bad.sum().item()} sums off, max err {(g - ref).abs().max().item()}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("ds,B,L", [(128, 2, 700), (96, 1, 3000), (64, 1, 32768)])
+def test_ssm_row_stats(dev, dtype, ds, B, L):
+    """The scan's per-row (sum, sum of squares) of its stored values over each 64-channel block
+    (the last one partial for ds=96), written at the given pair column of a wider buffer whose
+    other columns stay untouched; y unchanged by the option."""
+    _say("ssm row stats", dtype, ds, B, L)
+    projs, A_log = ssm_inputs(B, L, ds, dtype)
+    pd, ad = projs.to(dev), A_log.to(dev)
+    nb = _ops.ssm_stats_parts(ds)
+    st = torch.full((nb + 2, B * L, 2), 7.0, device=dev)
+    y = torch.empty(B, L, ds, device=dev, dtype=dtype)
+    y0 = torch.empty_like(y)
+    _ops.ssm(pd, ad, ds, y0)
+    _ops.ssm(pd, ad, ds, y, row_stats=st, stats_part=1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y0)
+    _check_stats(st[1:1 + nb].transpose(0, 1), _block_sums(y.cpu().reshape(B * L, ds), 64), "ssm row stats")
+    assert (st[0] == 7).all() and (st[1 + nb:] == 7).all()
+
+
+@pytest.mark.parametrize("dtype,B,L,dm,H,C,out_col", [
+    (torch.bfloat16, 1, 512, 256, 4, 64, 64), (torch.float32, 2, 256, 256, 8, 64, 64),
+    (torch.bfloat16, 1, 512, 512, 4, 128, 64), (torch.bfloat16, 2, 256, 256, 8, 64, 4),  # 8-byte store path
+    (torch.float32, 1, 384, 384, 4, 64, 64)])
+def test_slot_gate_row_stats(dev, dtype, B, L, dm, H, C, out_col):
+    """slot_gate's per-row (sum, sum of squares) of its stored values, one pair per head."""
+    _say("slot row stats", dtype, B, L, dm, H, C, out_col)
+    ds = 64
+    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, dtype, seed=L + dm)
+    pd = projs.to(dev)
+    out = torch.zeros(B, L, out_col + dm, device=dev, dtype=dtype)
+    ws = _ops.slot_workspace(pd, dm, H, C)
+    _ops.slot_state(pd, 3 * ds, gamma.to(dev), dm, H, C, ws)
+    st = torch.full((H + 1, B * L, 2), 7.0, device=dev)
+    _ops.slot_gate(pd, 3 * ds, gamma.to(dev), gn_w.to(dev), gn_b.to(dev), 1e-5, ws, out, out_col, dm, H, C,
+                   row_stats=st, stats_part=1)
+    vals = out[..., out_col:].cpu().reshape(B * L, dm)
+    _check_stats(st[1:].transpose(0, 1), _block_sums(vals, dm // H), "slot row stats")
+    assert (st[0] == 7).all()
+
+
+@pytest.mark.parametrize("M,N,K,mean", [
+    (300, 264, 1152, 0.3), (4096, 1024, 1152, 4.0), (513, 768, 832, 2.0), (17, 8, 64, 1.0), (1000, 2048, 2176, 0.0)])
+def test_rowln_gemm_stats(dev, M, N, K, mean):
+    """hdcm_rowln_gemm_stats_fwd with row statistics supplied as 64-column partial sums and the
+    weight row sums from hdcm_row_sums_fwd: the bound of test_rowln_gemm against torch fp32,
+    then in place."""
+    _say("rowln_gemm_stats", M, N, K, mean)
+    g = torch.Generator().manual_seed(M + N + K + 1)
+    c = (1.5 * torch.randn(M, K, generator=g) + mean).to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    ref = r.float() + torch.nn.functional.layer_norm(c.float(), (K,), eps=1e-5) @ W.float().t()
+    cd, Wd, rd = c.to(dev), W.to(dev), r.to(dev)
+    ws = _ops.row_sums(Wd)
+    torch.cuda.synchronize()
+    assert torch.allclose(ws.cpu().double(), W.double().sum(1), rtol=1e-5, atol=1e-4)
+    st = _block_sums(c, 64).float().transpose(0, 1).contiguous().to(dev)
+    out = _ops.rowln_gemm_stats(cd, Wd, ws, st, rd)
+    torch.cuda.synchronize()
+    err = (out.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
+    _ops.rowln_gemm_stats(cd, Wd, ws, st, rd, out=rd)  # out aliasing the residual
+    torch.cuda.synchronize()
+    assert torch.equal(rd.cpu(), out.cpu())
+
+
 def test_fused_out_proj_matches_unfused(dev):
     """A bf16 model forward with the LayerNorm folded into out_proj against the same model
     with the row LayerNorm kernel and addmm."""

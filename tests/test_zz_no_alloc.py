@@ -16,7 +16,7 @@ def _call(fn_name, projs, A_log, ds, y, hf, ws=None):
     lib = _ops.lib()
     B, L, P = projs.shape
     stream = torch.cuda.current_stream(projs.device).cuda_stream
-    args = [projs.data_ptr(), P, A_log.data_ptr(), None, y.data_ptr(), y.stride(1), hf.data_ptr()]
+    args = [projs.data_ptr(), P, A_log.data_ptr(), None, y.data_ptr(), y.stride(1), hf.data_ptr(), None, 0]
     if ws is not None:
         args += [ws.data_ptr(), ws.numel()]
     args += [B, L, ds, _ops._dtype(projs), stream]
@@ -49,6 +49,6 @@ def test_noalloc_rejects_inputs_beyond_its_scratch(dev):
     assert lib.hdcm_ssm_workspace_bytes(B, L, ds) > (8 << 20)
     projs = torch.empty(16, dtype=torch.bfloat16, device=dev)  # never read: rejected first
     st = lib.hdcm_ssm_fwd_noalloc(projs.data_ptr(), 3 * ds, projs.data_ptr(), None, projs.data_ptr(), ds, None,
-                                  B, L, ds, _ops.HDCM_BF16, torch.cuda.current_stream(dev).cuda_stream)
+                                  None, 0, B, L, ds, _ops.HDCM_BF16, torch.cuda.current_stream(dev).cuda_stream)
     assert st == ETOOBIG
     assert b"scratch" in lib.hdcm_strerror(st)
