@@ -320,12 +320,17 @@ int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_
   const int64_t nchunk = chunks_of(L);
   const dim3 rgrid((unsigned)((L + kRowsWPB * kRunRows - 1) / (kRowsWPB * kRunRows)), (unsigned)B);
 #define HDCM_BWD_ROWS(N)                                                                                         \
-  if (ng == N)                                                                                                   \
+  if (ng <= N)                                                                                                   \
     HDCM_LAUNCH((norm_conv_bwd_rows_kernel<T, N>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
                        g_bs, g_rs, (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)conv_w, (T*)dx, d_bs, d_rs, \
                        stats, (int)L, (int)D, eps);
+  // up to 4 groups per lane: one instance per count; fp32 rows of 1028 to 2048 columns (5 to
+  // 8 groups) share an 8-group instance whose lanes past the row idle (256 VGPRs + 108 AGPRs,
+  // no spills; bf16 rows up to 2048 columns fit in 4 groups)
   HDCM_BWD_ROWS(1)
-  else HDCM_BWD_ROWS(2) else HDCM_BWD_ROWS(3) else HDCM_BWD_ROWS(4) else return HDCM_EUNSUPPORTED;
+  else HDCM_BWD_ROWS(2) else HDCM_BWD_ROWS(3) else HDCM_BWD_ROWS(4) else if constexpr (sizeof(T) == 4) {
+    HDCM_BWD_ROWS(8) else return HDCM_EUNSUPPORTED;
+  } else return HDCM_EUNSUPPORTED;
 #undef HDCM_BWD_ROWS
   int st = hdcm_launch_status();
   if (st) return st;
@@ -358,7 +363,7 @@ extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, 
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && D > 0, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
-  HDCM_CHECK_ARG(D / E <= 4 * kWave, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(D <= 2048, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30 && (L + kChunk - 1) / kChunk <= 65535, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(hdcm_aligned16(ln_w) && hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w), HDCM_EALIGN);
   if (B == 0 || L == 0)  // no rows (strides unused): the parameter gradients are zero

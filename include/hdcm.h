@@ -84,7 +84,7 @@ int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t x_row_stri
  * d_conv_b [D].  Exact gradients of the forward, including the ln_b terms through the
  * LayerNorm of the zero rows before the sequence start; parameter gradients are summed in
  * a fixed order (deterministic).  ws: hdcm_norm_conv_bwd_workspace_bytes(B, L, D) bytes,
- * 256-byte aligned.  Needs D/(16/elt_size) <= 256.
+ * 256-byte aligned.  Needs D <= 2048.
  * Replaces: FusedNormConv1dFunction.backward -> _fused_norm_conv_bwd_kernel
  *           (hdcmamba/model.py:149-166, kernel model.py:74-124), which omits the ln_b
  *           terms of d_conv_w and d_ln_b and uses bf16-rounded row statistics.

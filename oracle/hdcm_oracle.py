@@ -464,11 +464,16 @@ def model_forward(sd, x, cfg: BlockCfg, n_layers, semantics="intended", layers=N
     return F.layer_norm(x, (cfg.d_model,), sd["norm_final.weight"], sd["norm_final.bias"], 1e-5)
 
 
-def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None, n_prefill=None):
+def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None, n_prefill=None,
+               positions=None):
     """UniversalLM.forward, HdcMamba arm (train_fineweb.py:86-94): embedding, backbone,
-    norm_f, tied lm_head.  ``n_prefill`` as in model_forward."""
+    norm_f, tied lm_head.  ``n_prefill`` as in model_forward.  With ``positions`` (a list of
+    token positions) the head runs on those positions only: logits [B, len(positions), V]
+    (the backbone still runs over the whole sequence)."""
     x = F.embedding(ids, sd["embedding.weight"])
     x = model_forward(_sub(sd, "backbone."), x, cfg, n_layers, semantics, layers, n_prefill)
+    if positions is not None:
+        x = x[:, list(positions)]
     x = F.layer_norm(x, (cfg.d_model,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)
     return F.linear(x, sd["embedding.weight"])
 

@@ -214,3 +214,29 @@ def test_empty_inputs(dev):
     ref = oracle.norm_conv(xr, w.detach().cpu(), b.detach().cpu(), cw.detach().cpu(), cb.detach().cpu(), 1e-5)
     ref.sum().backward()
     assert max_rel(x.grad, xr.grad) <= 1e-4
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("name", ["lm_c3", "lm_c4"])
+def test_lm_logits_against_oracle(dev, name):
+    """The whole headline LM end to end in bf16 (12 layers d_model 768 at B=8 x 4096, and 24
+    layers d_model 1024 d_state 128 at B=1 x 32768; vocab 50304, default init): the logits
+    at 64 positions per sequence (the last 16 and 48 drawn at random) against the oracle's
+    LM forward (the whole backbone on the CPU, the head at those positions), normwise."""
+    cfg = WORKLOADS[name]
+    print("lm end to end", name, flush=True)
+    lm = make_lm(name, seed=5).to(torch.bfloat16)
+    ids = lm_input(name, seed=6)
+    L = ids.shape[1]
+    g = torch.Generator().manual_seed(7)
+    pos = sorted(set(torch.randint(0, L - 16, (48,), generator=g).tolist()) | set(range(L - 16, L)))
+    with torch.no_grad():
+        logits = lm.to(dev)(ids.to(dev))
+    got = logits[:, pos].float().cpu()
+    del logits
+    torch.cuda.empty_cache()
+    ref = oracle.lm_forward(_sd(lm), ids, oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"],
+                                                          cfg["chunk"]), cfg["n_layers"], positions=pos)
+    print("max rel", max_rel(got, ref), flush=True)
+    assert_close_normwise(got, ref, torch.bfloat16, f"{name} logits")
+
