@@ -124,22 +124,103 @@ def kernel_table(cfg, tokens, times):
     return out
 
 
-def roofline_of(k, traffic):
-    """The bench line's roofline object for one kernel_table entry."""
+def roofline_of(k, traffic, profile_us=None):
+    """The bench line's roofline object for one kernel_table entry; with `profile_us` (the
+    kernel's mean duration in the committed rocprofv3 kernel trace of this bench command),
+    also the fraction that duration gives."""
     if k["bound"] == "mfma":
-        return {"bound": "mfma", "achieved": k["TFLOP/s"], "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s",
-                "frac": k["frac"], "traffic": traffic, "us": k["us"], "flops_per_launch": k["flops_per_launch"]}
-    return {"bound": "hbm", "achieved": k["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": k["frac"],
-            "traffic": traffic, "us": k["us"], "bytes_per_launch": k["bytes_per_launch"]}
+        r = {"bound": "mfma", "achieved": k["TFLOP/s"], "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s",
+             "frac": k["frac"], "traffic": traffic, "us": k["us"], "flops_per_launch": k["flops_per_launch"]}
+        work, peak, scale = k["flops_per_launch"], MFMA_PEAK_TFS, 1e12
+    else:
+        r = {"bound": "hbm", "achieved": k["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": k["frac"],
+             "traffic": traffic, "us": k["us"], "bytes_per_launch": k["bytes_per_launch"]}
+        work, peak, scale = k["bytes_per_launch"], HBM_PEAK_GBS, 1e9
+    if profile_us:
+        r["profile_us"] = profile_us
+        r["profile_frac"] = round(work / (profile_us * 1e-6) / scale / peak, 4)
+    return r
 
 
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "slot_gate_lm_c4_traffic.md")
-TRAFFIC_KEY = "traffic_bytes_per_launch:"
+PROFILES = os.path.join(ROOT, "profiles")
+TRAFFIC_SUMMARY = os.path.join(PROFILES, "lm_c4_forward_traffic.md")
+STATS_SUMMARY = os.path.join(PROFILES, "lm_c4_forward_kernel_stats.md")
+MFMA_SUMMARY = os.path.join(PROFILES, "lm_c4_forward_mfma.md")
+SOURCE_KEY = "kernel_sources_sha256:"
+
+# bench.py kernel key -> start of the kernel's name in rocprofv3 output (template arguments
+# removed); the out_proj GEMM of the forward is the statistics variant (EPI_ROWSTATS = 2)
+KERNEL_NAMES = {"norm_conv": "norm_conv_kernel<", "ssm": "ssm_scan_kernel<", "slot_state": "slot_state_kernel<",
+                "slot_scan": "slot_scan_kernel<", "slot_gate": "slot_gate_kernel<", "rowln": "rowln_kernel<",
+                "out_proj": "gemm_bt_kernel<2,"}
 
 
 def _short_name(n):
     n = n.replace("void ", "").replace("(anonymous namespace)::", "")
     return n.split("(")[0]
+
+
+def _kernel_key(name):
+    for key, prefix in KERNEL_NAMES.items():
+        if name.startswith(prefix):
+            return key
+    return None
+
+
+def source_hash():
+    """sha256 over the HIP sources and headers the library's kernels are built from and the
+    package's Python (which decides the launch sequence): a stored profile is used only while
+    these are unchanged."""
+    import glob
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(ROOT, "hdcmamba_amd", "csrc", "*.hip")) +
+                   glob.glob(os.path.join(ROOT, "hdcmamba_amd", "csrc", "*.h")) +
+                   glob.glob(os.path.join(ROOT, "hdcmamba_amd", "*.py")) +
+                   [os.path.join(ROOT, "include", "hdcm.h")])
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def _metric_lines(metric, values):
+    """Machine-readable lines of a profile summary: '<metric>: <kernel> <value>'."""
+    return [f"{metric}: {k} {v}" for k, v in sorted(values.items())]
+
+
+def stored_metric(path, metric):
+    """{kernel: value} of `metric` in a committed profile summary, or {} when the summary is
+    missing or was made from other kernel sources than the ones in this tree."""
+    if not os.path.exists(path):
+        return {}
+    vals, src = {}, None
+    with open(path) as f:
+        for line in f:
+            if line.startswith(SOURCE_KEY):
+                src = line.split(":", 1)[1].strip()
+            elif line.startswith(metric + ":"):
+                f = line.split(":", 1)[1].split()
+                if len(f) == 2:  # '<kernel> <value>' (older summaries held one bare number)
+                    vals[f[0]] = float(f[1])
+    return vals if src == source_hash() else {}
+
+
+def _read_pmc(path):
+    """{(dispatch id): {counter: value}, ...} and {dispatch id: short kernel name} of a
+    rocprofv3 --pmc counter_collection.csv."""
+    import collections
+    import csv
+
+    vals, names = collections.defaultdict(dict), {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            d = int(r["Dispatch_Id"])
+            vals[d][r["Counter_Name"]] = float(r["Counter_Value"])
+            names[d] = _short_name(r["Kernel_Name"])
+    return vals, names
 
 
 def pmc_summary(fetch_csv, write_csv, copy_bytes):
@@ -148,14 +229,13 @@ def pmc_summary(fetch_csv, write_csv, copy_bytes):
     runtime's copy kernel for the copy of known size (`copy_bytes`) in the same run.
     Returns markdown text."""
     import collections
-    import csv
 
     def read(path, counter):
+        vals, names = _read_pmc(path)
         agg = collections.defaultdict(list)
-        with open(path) as f:
-            for r in csv.DictReader(f):
-                if r["Counter_Name"] == counter:
-                    agg[_short_name(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        for d, c in vals.items():
+            if counter in c:
+                agg[names[d]].append(c[counter])
         return agg
 
     def scale(agg, counter):
@@ -168,58 +248,101 @@ def pmc_summary(fetch_csv, write_csv, copy_bytes):
     ff, fw = scale(fa, "FETCH_SIZE"), scale(wa, "WRITE_SIZE")
     lines = ["| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB per dispatch (scaled) |",
              "|---|---:|---:|---:|---:|"]
-    out = {}
+    out, keyed = {}, {}
     for k in sorted(set(fa) & set(wa), key=lambda k: -sum(fa[k]) / len(fa[k])):
         f, w = sum(fa[k]) / len(fa[k]), sum(wa[k]) / len(wa[k])
         out[k] = (f * ff + w * fw) * 1024
         lines.append(f"| {k[:70]} | {len(fa[k])} | {f:.1f} | {w:.1f} | {out[k] / 1e6:.2f} |")
-    gate = [k for k in out if k.startswith("slot_gate_kernel")]
-    head = [f"copy calibration ({copy_bytes} bytes): FETCH_SIZE x {ff:.4f}, WRITE_SIZE x {fw:.4f}", ""]
-    if gate:
-        head += [f"{TRAFFIC_KEY} {round(out[gate[0]])}", f"{SOURCE_KEY} {slot_source_hash()}", ""]
+        key = _kernel_key(k)
+        if key:
+            keyed[key] = round(out[k])
+    head = [f"copy calibration ({copy_bytes} bytes): FETCH_SIZE x {ff:.4f}, WRITE_SIZE x {fw:.4f}", "",
+            f"{SOURCE_KEY} {source_hash()}"] + _metric_lines("traffic_bytes_per_launch", keyed) + [""]
+    return "\n".join(head + lines) + "\n"
+
+
+def mfma_summary(pmc_csv):
+    """Per-kernel MFMA use from a rocprofv3 --pmc run of MfmaUtil (rocprofiler's derived metric:
+    SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, percent), SQ_INSTS_VALU_MFMA_MOPS_BF16
+    and SQ_INSTS_VALU_MFMA_MOPS_F32 (x 512 = FLOPs).  Returns markdown text."""
+    import collections
+
+    vals, names = _read_pmc(pmc_csv)
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d, c in vals.items():
+        for ctr, v in c.items():
+            agg[names[d]][ctr].append(v)
+    lines = ["| kernel | dispatches | MFMA busy % | bf16 MFMA GFLOP per dispatch | fp32 MFMA GFLOP per dispatch |",
+             "|---|---:|---:|---:|---:|"]
+    keyed, order = {}, []
+    for k, c in agg.items():
+        if "MfmaUtil" not in c:
+            continue
+        util = sum(c["MfmaUtil"]) / len(c["MfmaUtil"])
+        bf = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0])) / max(1, len(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0]))) * 512
+        f32 = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", [0])) / max(1, len(c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", [0]))) * 512
+        order.append((-util, k, len(c["MfmaUtil"]), util, bf, f32))
+        key = _kernel_key(k)
+        if key:
+            keyed[key] = round(util / 100, 4)
+    for _, k, n, util, bf, f32 in sorted(order):
+        if util > 0 or bf > 0:
+            lines.append(f"| {k[:70]} | {n} | {util:.1f} | {bf / 1e9:.2f} | {f32 / 1e9:.3f} |")
+    head = [f"{SOURCE_KEY} {source_hash()}"] + _metric_lines("mfma_busy", keyed) + [""]
+    return "\n".join(head + lines) + "\n"
+
+
+def trace_summary(trace_csv, steps, warmup, layers=24, capture_warmup=2):
+    """Per-kernel mean durations of a rocprofv3 --kernel-trace run of this bench by phase: the
+    recorded graph's replays (warmup + steps forwards after the capture's warm-up forwards) and
+    the event-timed eager forwards (the last min(steps, 5)), for the kernels launched once per
+    layer.  Returns markdown text with 'graph_us' and 'timed_us' lines."""
+    import collections
+    import csv
+
+    k_steps = max(1, min(steps, 5))
+    fwd = capture_warmup + warmup + steps + 1 + k_steps  # forwards of the run, in order
+    by = collections.defaultdict(list)
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            key = _kernel_key(_short_name(r["Kernel_Name"]))
+            if key:
+                by[key].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    lines = ["| kernel | launches | all (us) | graph replays (us) | timed eager forwards (us) |",
+             "|---|---:|---:|---:|---:|"]
+    graph, timed = {}, {}
+    for key in KERNEL_NAMES:
+        v = sorted(by.get(key, []))
+        if len(v) != fwd * layers:
+            continue
+        d = [(e - s) / 1e3 for s, e in v]
+        g = d[capture_warmup * layers:(capture_warmup + warmup + steps) * layers]
+        t = d[(fwd - k_steps) * layers:]
+        graph[key], timed[key] = round(sum(g) / len(g), 2), round(sum(t) / len(t), 2)
+        lines.append(f"| {key} | {len(d)} | {sum(d) / len(d):.2f} | {graph[key]:.2f} | {timed[key]:.2f} |")
+    head = ([f"{SOURCE_KEY} {source_hash()}"] + _metric_lines("graph_us", graph) + _metric_lines("timed_us", timed)
+            + [""])
     return "\n".join(head + lines) + "\n"
 
 
 def stats_summary(stats_csv):
-    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv."""
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv, with the mean
+    duration of the bench's kernels as machine-readable lines."""
     import csv
 
     with open(stats_csv) as f:
         rows = list(csv.DictReader(f))
     lines = ["| kernel | calls | avg us | share |", "|---|---:|---:|---:|"]
+    keyed = {}
     for r in rows:
-        lines.append(f"| {_short_name(r['Name'])[:70]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} "
-                     f"| {float(r['Percentage']):.1f}% |")
-    return "\n".join(lines) + "\n"
-
-
-SOURCE_KEY = "slot_sources_sha256:"
-
-
-def slot_source_hash():
-    """sha256 over the sources that define slot_gate's kernels and launch plan."""
-    import hashlib
-
-    h = hashlib.sha256()
-    for rel in ("hdcmamba_amd/csrc/slot.hip", "hdcmamba_amd/csrc/hdcm_common.h"):
-        with open(os.path.join(ROOT, rel), "rb") as f:
-            h.update(f.read())
-    return h.hexdigest()
-
-
-def stored_traffic(workload):
-    """HBM bytes per slot_gate launch recorded by the counter runs for the L=32768 LM, or None
-    when the summary was made from other slot sources than the ones in this tree."""
-    if workload != "lm_c4" or not os.path.exists(TRAFFIC_SUMMARY):
-        return None
-    traffic, src = None, None
-    with open(TRAFFIC_SUMMARY) as f:
-        for line in f:
-            if line.startswith(TRAFFIC_KEY):
-                traffic = int(line.split(":", 1)[1])
-            elif line.startswith(SOURCE_KEY):
-                src = line.split(":", 1)[1].strip()
-    return traffic if src == slot_source_hash() else None
+        name = _short_name(r["Name"])
+        avg = float(r["AverageNs"]) / 1e3
+        lines.append(f"| {name[:70]} | {r['Calls']} | {avg:.1f} | {float(r['Percentage']):.1f}% |")
+        key = _kernel_key(name)
+        if key and key not in keyed:
+            keyed[key] = round(avg, 2)
+    head = [f"{SOURCE_KEY} {source_hash()}"] + _metric_lines("avg_us", keyed) + [""]
+    return "\n".join(head + lines) + "\n"
 
 
 def cpu_baseline(model, ids_gpu, cfg, budget_s):
@@ -391,9 +514,21 @@ def main():
                          "(FETCH_SIZE, WRITE_SIZE) and exit; needs no GPU")
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
                     help="print the per-kernel table of a rocprofv3 --stats run and exit")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="print the per-phase kernel durations of a rocprofv3 --kernel-trace run of this bench "
+                         "(made with the --steps and --warmup given here) and exit")
+    ap.add_argument("--mfma-summary", metavar="PMC_CSV",
+                    help="print the MFMA-use table of a rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 "
+                         "SQ_INSTS_VALU_MFMA_MOPS_F32 run of this bench and exit; needs no GPU")
     args = ap.parse_args()
     if args.stats_summary:
         sys.stdout.write(stats_summary(args.stats_summary))
+        return
+    if args.mfma_summary:
+        sys.stdout.write(mfma_summary(args.mfma_summary))
+        return
+    if args.trace_summary:
+        sys.stdout.write(trace_summary(args.trace_summary, args.steps, args.warmup))
         return
     if args.pmc_summary:
         # the residual-stream copy of the embedding output: B*L*d_model bf16 values
@@ -447,7 +582,12 @@ def main():
         # HIP events from its own dispatch timestamps (hdcm_time_launches; launches inside a
         # graph replay cannot carry events).  The events add nothing to the stream, so these
         # forwards also give the eager rate.
+        # The scan runs in sequence with the slot kernels here, as in the recorded graph, so each
+        # kernel is timed alone (eager forwards otherwise overlap it with the slot pre-pass).
         k_steps = max(1, min(args.steps, 5))
+        from hdcmamba_amd.model import HdcMamba9v3Block
+        overlap = HdcMamba9v3Block.ssm_overlap
+        HdcMamba9v3Block.ssm_overlap = "none"
         model(inp)
         torch.cuda.synchronize()
         _ops.timer.active = set(KERNELS)
@@ -457,19 +597,44 @@ def main():
         torch.cuda.synchronize()
         t3 = time.perf_counter()
         _ops.timer.active = set()
+        HdcMamba9v3Block.ssm_overlap = overlap
     times = _ops.timer.collect()
     sec = t1 - t0
     ms_per_step = sec / args.steps * 1e3
     value = tokens * args.steps / sec
     eager_ms = (t3 - t2) / k_steps * 1e3
     kernels = kernel_table(cfg, tokens, times)
-    roofline = roofline_of(kernels["slot_gate"], stored_traffic(args.workload))
+    # figures of the committed rocprofv3 summaries of this command (profiles/), when they were
+    # made from the kernel sources in this tree: HBM bytes per launch (FETCH_SIZE + WRITE_SIZE),
+    # mean kernel-trace durations, MFMA busy fractions
+    stored = args.workload == "lm_c4" and args.fused_out_proj == "on"
+    traffic = stored_metric(TRAFFIC_SUMMARY, "traffic_bytes_per_launch") if stored else {}
+    prof_us = stored_metric(STATS_SUMMARY, "timed_us") if stored else {}
+    graph_us = stored_metric(STATS_SUMMARY, "graph_us") if stored else {}
+    mfma = stored_metric(MFMA_SUMMARY, "mfma_busy") if stored else {}
+    for k, v in kernels.items():
+        if k in prof_us:
+            v["profile_us"] = prof_us[k]
+        if k in graph_us:
+            v["graph_us"] = graph_us[k]
+        if k in mfma:
+            v["mfma_busy"] = mfma[k]
+    roofline = roofline_of(kernels["slot_gate"], traffic.get("slot_gate"), prof_us.get("slot_gate"))
     # the slot operator as a whole (state pre-pass, segment scan, gate pass) against the
     # gate pass's algorithmic bytes (q, k, v, gate read once, output written once)
-    roofline_slot_op = roofline_of(kernels["slot_op"], None) if "slot_op" in kernels else None
+    roofline_slot_op = None
+    if "slot_op" in kernels:
+        parts = ("slot_state", "slot_scan", "slot_gate")
+        op_traffic = sum(traffic[p] for p in parts) if all(p in traffic for p in parts) else None
+        op_us = round(sum(prof_us[p] for p in parts), 2) if all(p in prof_us for p in parts) else None
+        roofline_slot_op = roofline_of(kernels["slot_op"], op_traffic, op_us)
     # the fused out_proj (LayerNorm folded into the GEMM) is the largest kernel of this build by
     # time; it is MFMA-bound, so its roofline is FLOPs against the bf16 dense peak
-    roofline_out_proj = roofline_of(kernels["out_proj"], None) if "out_proj" in kernels else None
+    roofline_out_proj = None
+    if "out_proj" in kernels:
+        roofline_out_proj = roofline_of(kernels["out_proj"], traffic.get("out_proj"), prof_us.get("out_proj"))
+        if "out_proj" in mfma:
+            roofline_out_proj["mfma_busy"] = mfma["out_proj"]
 
     forward_summary = None
     if args.workload.startswith("lm"):
@@ -505,7 +670,10 @@ def main():
         "forward": forward_summary,
         "timing": {"steps": "HIP graph replays of the whole forward" if use_graph else "eager forwards",
                    "kernels": (f"HIP events recorded by each custom kernel's own dispatch (begin and end "
-                               f"timestamps, hipExtLaunchKernel) over {k_steps} eager forwards; mean per launch"),
+                               f"timestamps, hipExtLaunchKernel) over {k_steps} eager forwards with the scan in "
+                               f"sequence with the slot kernels (as in the recorded graph); mean per launch. "
+                               f"profile_us: the same launches in the committed kernel trace; graph_us: that "
+                               f"trace's graph replays"),
                    "eager_ms_per_step": round(eager_ms, 3)},
         "gemm_solutions": (f"TunableOp file, {n_tuned} recorded GEMM signatures" if n_tuned
                            else "library default heuristics"),

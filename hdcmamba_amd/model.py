@@ -183,6 +183,14 @@ class HdcMamba9v3Block(nn.Module):
     ``_fused_out``); otherwise as a row LayerNorm kernel and addmm.
     """
 
+    # where the SSM's launch overlaps the slot kernels (see _mixer): "auto" runs it in sequence
+    # while a HIP graph is being recorded and beside the slot pre-pass and scan otherwise.
+    # Measured at the 24-layer d_model=1024 L=32768 forward: recorded graph 14.46 ms per
+    # forward in sequence against 14.59 overlapped (with no launch gaps to fill, the scan's
+    # workgroups only slow the pre-pass: 25 + 55 us against 24 + 28 us); eager forwards 15.14
+    # overlapped against 15.65 in sequence.
+    ssm_overlap = "auto"
+
     def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False,
                  fused_out_proj=True):
         super().__init__()
@@ -226,26 +234,42 @@ class HdcMamba9v3Block(nn.Module):
         x_conv = fused_norm_conv1d_trainable(x, self.norm, self.conv1d)
         projs = F.linear(x_conv, self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype))
         combined = torch.empty(B, L, ds + dm, device=x.device, dtype=dtype)
-        # The SSM (latency-bound: three short launches) and the slot kernels read projs
-        # and write disjoint columns of `combined`, so the SSM runs on a side stream next
-        # to the slot state pre-pass and scan.  It joins before slot_gate, which then has
-        # the GPU to itself (overlapping the gate as well measured the same forward time
-        # within noise).  The join orders every later use (and the allocator's reuse) of
-        # projs and combined after the SSM.
+        # The SSM and the slot kernels read projs and write disjoint columns of `combined`,
+        # so the SSM may run on a side stream beside some of the slot kernels (ssm_overlap:
+        # "state" = beside the state pre-pass and scan, "after_state" = beside the scan and
+        # the gate pass, "gate" = beside all three, "none" = before them, the main stream
+        # waiting for it; "auto" = "none" under graph capture, else "state").  The
+        # join before the return orders every later use (and the allocator's reuse) of projs
+        # and combined after the SSM.
         main = torch.cuda.current_stream(x.device)
-        side = _ops.side_stream(x.device)
-        side.wait_stream(main)
-        with torch.cuda.stream(side):
-            _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h,
-                     row_stats=row_stats, stats_part=0)
+        mode = self.ssm_overlap
+        if mode == "auto":
+            mode = "none" if torch.cuda.is_current_stream_capturing() else "state"
+        side = _ops.side_stream(x.device)  # one stream per device: the scan's workspace is kept per stream
+
+        def run_ssm():
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                _ops.ssm(projs, self.A_log, ds, combined[..., :ds], h_final=None if state is None else state.h,
+                         row_stats=row_stats, stats_part=0)
+            if mode == "none":
+                main.wait_stream(side)
+
         gamma = self.gamma_buf.to(dtype)
         q_col = 3 * ds
         ws = _ops.slot_workspace(projs, dm, H, C)
+        if mode != "after_state":
+            run_ssm()
         _ops.slot_state(projs, q_col, gamma, dm, H, C, ws)
-        main.wait_stream(side)
+        if mode == "after_state":
+            run_ssm()
+        if mode == "state":
+            main.wait_stream(side)
         _ops.slot_gate(projs, q_col, gamma, self.group_norm.weight, self.group_norm.bias, 1e-5, ws,
                        combined, ds, dm, H, C, S_final=None if state is None else state.S_prev,
                        row_stats=row_stats, stats_part=_ops.ssm_stats_parts(ds))
+        if mode in ("gate", "after_state"):
+            main.wait_stream(side)
         if normalize:
             _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
