@@ -11,9 +11,10 @@
 //
 // Forward (ssm_scan_kernel): one launch that reads every input once.  A workgroup owns a
 // tile of TR rows x 64 channels.  A thread holds 4 consecutive rows x one 16-byte channel
-// group, scans them serially in registers, and the row groups are combined by a lane scan
-// (shuffles) and across waves through LDS.  The workgroup then publishes its tile total
-// (A, H) per channel and folds the totals of all earlier tiles of its sequence into the
+// group and scans them serially in registers; the row groups' totals are folded through LDS
+// in eight segments, and the tile total (A, H) per channel is published after two barriers,
+// before the row groups' prefixes within the tile are formed.  The workgroup then folds the
+// totals of all earlier tiles of its sequence into the
 // state entering the tile (decoupled look-back over totals, no inclusive chain), applies it
 // to the rows it still holds in registers and stores y once.  Totals are published as 64-bit
 // agent-scope atomic words {value, tag} that bypass the non-coherent per-XCD L2s, one word
@@ -306,7 +307,7 @@ __device__ __forceinline__ void pairs_of(const uint4 (&g)[3], const float (&negA
 }
 
 // One row folded into this thread's running total (ca, ch), rows in order.  Every
-// multiply-add here and in combine_tile is an explicit fmaf, so a tile total has identical
+// multiply-add here and in combine_total is an explicit fmaf, so a tile total has identical
 // bits wherever it is computed (by the tile's owner, or by a workgroup computing it on the
 // owner's behalf with tile_total_streamed).
 template <typename T>
@@ -322,29 +323,106 @@ __device__ __forceinline__ void fold_row(const uint4 (&g)[3], const float (&negA
   }
 }
 
-// LDS of the cross-thread part of a tile: one (A, H) pair per row group and channel, the
-// segment totals, and the tile total.
+// LDS of the cross-thread part of a tile: one (A, H) pair per channel and row group, stored
+// channel-major with an odd pitch (the threads of a segment read 64 consecutive channels of
+// one row group, and the threads of a row group write their channels, on distinct banks), and
+// the segment totals.
 constexpr int kMaxRG = kScanThreads / (kScanCh / 8);  // row groups of the bf16 tile (the most)
 constexpr int kSeg = kScanThreads / kScanCh;          // row-group segments, one thread per channel each
+constexpr int kRGPitch = kMaxRG + 1;
 struct ScanLds {
-  float rg[kMaxRG][kScanCh][2];
+  float rgA[kScanCh][kRGPitch];
+  float rgH[kScanCh][kRGPitch];
   float seg[kSeg][kScanCh][2];
-  float tot[kScanCh][2];
 };
 
+// The tile total from each thread's total (ca, ch) over its rows: the row groups' pairs go to
+// LDS, thread (segment s, channel c) folds its run of RGS row groups in order (kept in va, vh
+// for combine_prefix), and the threads of segment 0 (tid < 64, channel tid) fold the segment
+// totals in order into (tA, tH).  Two barriers.
 template <typename T>
-__device__ __forceinline__ void combine_tile(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N], int nch,
-                                             float (&xa)[Vec<T>::N], float (&xh)[Vec<T>::N], float (&ta)[Vec<T>::N],
-                                             float (&th)[Vec<T>::N], ScanLds* lds);
+__device__ __forceinline__ void combine_total(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N],
+                                              float (&va)[ScanShape<T>::RG / kSeg],
+                                              float (&vh)[ScanShape<T>::RG / kSeg], float& tA, float& tH,
+                                              ScanLds* lds) {
+  using S = ScanShape<T>;
+  constexpr int E = S::E, CG = S::CG, RG = S::RG;
+  constexpr int RGS = RG / kSeg;  // row groups per segment
+  static_assert(RG % kSeg == 0 && RG <= kMaxRG, "row-group segments");
+  const int tid = threadIdx.x, cg = tid % CG, rg = tid / CG;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    lds->rgA[cg * E + e][rg] = ca[e];
+    lds->rgH[cg * E + e][rg] = ch[e];
+  }
+  __syncthreads();
+  const int c = tid % kScanCh, s = tid / kScanCh;
+  float sa = 1.f, sh = 0.f;
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    va[k] = lds->rgA[c][s * RGS + k];
+    vh[k] = lds->rgH[c][s * RGS + k];
+  }
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    sh = fmaf(va[k], sh, vh[k]);
+    sa = sa * va[k];
+  }
+  lds->seg[s][c][0] = sa;
+  lds->seg[s][c][1] = sh;
+  __syncthreads();
+  tA = 1.f, tH = 0.f;
+  if (s == 0) {
+#pragma unroll
+    for (int k = 0; k < kSeg; ++k) {
+      const float ka = lds->seg[k][c][0], kh = lds->seg[k][c][1];
+      tH = fmaf(ka, tH, kh);
+      tA = tA * ka;
+    }
+  }
+}
 
-// A tile's total (threads of row group 0: their E channels) with the rows read one at a time
-// (few registers in use): the kernel's own fold, row by row in the same order, then
-// combine_tile, hence the same bits.
+// After combine_total (same va, vh): each row group's exclusive prefix within the tile, handed
+// back to its threads as (xa, xh) for their E channels.  Two barriers; the LDS is free after.
+template <typename T>
+__device__ __forceinline__ void combine_prefix(const float (&va)[ScanShape<T>::RG / kSeg],
+                                               const float (&vh)[ScanShape<T>::RG / kSeg], float (&xa)[Vec<T>::N],
+                                               float (&xh)[Vec<T>::N], ScanLds* lds) {
+  using S = ScanShape<T>;
+  constexpr int E = S::E, CG = S::CG, RGS = S::RG / kSeg;
+  const int tid = threadIdx.x;
+  const int c = tid % kScanCh, s = tid / kScanCh;
+  float pa = 1.f, ph = 0.f;  // segments before s
+  for (int k = 0; k < s; ++k) {
+    const float ka = lds->seg[k][c][0], kh = lds->seg[k][c][1];
+    ph = fmaf(ka, ph, kh);
+    pa = pa * ka;
+  }
+#pragma unroll
+  for (int k = 0; k < RGS; ++k) {
+    lds->rgA[c][s * RGS + k] = pa;
+    lds->rgH[c][s * RGS + k] = ph;
+    ph = fmaf(va[k], ph, vh[k]);
+    pa = pa * va[k];
+  }
+  __syncthreads();
+  const int cg = tid % CG, rg = tid / CG;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    xa[e] = lds->rgA[cg * E + e][rg];
+    xh[e] = lds->rgH[cg * E + e][rg];
+  }
+  __syncthreads();  // the LDS is reused
+}
+
+// A tile's total (threads tid < 64: channel tid) with the rows read one at a time (few
+// registers in use): the kernel's own fold, row by row in the same order, then
+// combine_total, hence the same bits.
 template <typename T>
 __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs, int64_t prs, int64_t rowbase,
                                                     int tile, int c0, int nch, int L, int ds,
-                                                    const float (&negA)[Vec<T>::N], float (&ta)[Vec<T>::N],
-                                                    float (&th)[Vec<T>::N], ScanLds* lds) {
+                                                    const float (&negA)[Vec<T>::N], float& tA, float& tH,
+                                                    ScanLds* lds) {
   using S = ScanShape<T>;
   constexpr int E = S::E;
   const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
@@ -359,90 +437,19 @@ __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs,
     const uint4 g[3] = {ldg16(p), ldg16(p + ds), ldg16(p + 2 * ds)};
     fold_row<T>(g, negA, cok && r0 + r < L, ca, ch);
   }
-  float xa[E], xh[E];
-  combine_tile<T>(ca, ch, nch, xa, xh, ta, th, lds);
-}
-
-// The cross-thread part of a tile, from each thread's total (ca, ch) over its rows: the row
-// groups' pairs go to LDS, thread (segment s, channel c) folds its run of row groups in
-// order, the segment totals are folded in order, and each row group gets back its exclusive
-// prefix.  Yields this thread's exclusive prefix (xa, xh) within the tile and (threads of
-// row group 0) the tile total (ta, th) of their E channels.
-template <typename T>
-__device__ __forceinline__ void combine_tile(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N], int nch,
-                                             float (&xa)[Vec<T>::N], float (&xh)[Vec<T>::N], float (&ta)[Vec<T>::N],
-                                             float (&th)[Vec<T>::N], ScanLds* lds) {
-  using S = ScanShape<T>;
-  constexpr int E = S::E, CG = S::CG, RG = S::RG;
-  constexpr int RGS = RG / kSeg;  // row groups per segment
-  static_assert(RG % kSeg == 0 && RG <= kMaxRG, "row-group segments");
-  const int tid = threadIdx.x, cg = tid % CG, rg = tid / CG;
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    lds->rg[rg][cg * E + e][0] = ca[e];
-    lds->rg[rg][cg * E + e][1] = ch[e];
-  }
-  __syncthreads();
-  const int c = tid % kScanCh, s = tid / kScanCh;
-  float va[RGS], vh[RGS];
-  float sa = 1.f, sh = 0.f;
-#pragma unroll
-  for (int k = 0; k < RGS; ++k) {
-    va[k] = lds->rg[s * RGS + k][c][0];
-    vh[k] = lds->rg[s * RGS + k][c][1];
-  }
-#pragma unroll
-  for (int k = 0; k < RGS; ++k) {
-    sh = fmaf(va[k], sh, vh[k]);
-    sa = sa * va[k];
-  }
-  lds->seg[s][c][0] = sa;
-  lds->seg[s][c][1] = sh;
-  __syncthreads();
-  float pa = 1.f, ph = 0.f;  // segments before s
-  for (int k = 0; k < s; ++k) {
-    const float ka = lds->seg[k][c][0], kh = lds->seg[k][c][1];
-    ph = fmaf(ka, ph, kh);
-    pa = pa * ka;
-  }
-#pragma unroll
-  for (int k = 0; k < RGS; ++k) {
-    lds->rg[s * RGS + k][c][0] = pa;
-    lds->rg[s * RGS + k][c][1] = ph;
-    ph = fmaf(va[k], ph, vh[k]);
-    pa = pa * va[k];
-  }
-  if (s == kSeg - 1) {
-    lds->tot[c][0] = pa;
-    lds->tot[c][1] = ph;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int e = 0; e < E; ++e) {
-    xa[e] = lds->rg[rg][cg * E + e][0];
-    xh[e] = lds->rg[rg][cg * E + e][1];
-    ta[e] = rg == 0 ? lds->tot[cg * E + e][0] : 1.f;
-    th[e] = rg == 0 ? lds->tot[cg * E + e][1] : 0.f;
-  }
+  float va[S::RG / kSeg], vh[S::RG / kSeg];
+  combine_total<T>(ca, ch, va, vh, tA, tH, lds);
   __syncthreads();  // the LDS is reused
 }
 
-// The tile total of this thread's channels, published for later tiles (row group 0 only).
-template <typename T>
+// The tile total of channel tid (< 64), published for later tiles.
 __device__ __forceinline__ void publish_total(unsigned long long* words, int64_t seq, int ntiles, int tile,
-                                              int nch, const float (&ta)[Vec<T>::N], const float (&th)[Vec<T>::N],
-                                              unsigned tag) {
-  using S = ScanShape<T>;
-  const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
-  if (rg != 0) return;
-#pragma unroll
-  for (int e = 0; e < S::E; ++e) {
-    const int c = cg * S::E + e;
-    if (c >= nch) continue;
-    unsigned long long* p = words + 2 * ((seq * kScanCh + c) * ntiles + tile);
-    __hip_atomic_store(p, pack_word(ta[e], tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(p + 1, pack_word(th[e], tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+                                              int nch, float tA, float tH, unsigned tag) {
+  const int c = threadIdx.x;
+  if (c >= nch) return;  // also every thread past the first 64 (nch <= 64)
+  unsigned long long* p = words + 2 * ((seq * kScanCh + c) * ntiles + tile);
+  __hip_atomic_store(p, pack_word(tA, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(p + 1, pack_word(tH, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Compute and publish, with this call's tag, the totals of the tiles j0 + k for the set bits
@@ -453,13 +460,12 @@ __device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int
                                                 const float (&negA)[Vec<T>::N], unsigned long long* words, int64_t seq,
                                                 int64_t rowbase, int c0, int nch, int L, int ds, int ntiles, int j0,
                                                 unsigned long long missing, unsigned tag, ScanLds* lds) {
-  constexpr int E = Vec<T>::N;
   while (missing != 0) {
     const int jm = j0 + __builtin_ctzll(missing);
     missing &= missing - 1;
-    float ta[E], th[E];
-    tile_total_streamed<T>(projs, prs, rowbase, jm, c0, nch, L, ds, negA, ta, th, lds);
-    publish_total<T>(words, seq, ntiles, jm, nch, ta, th, tag);
+    float tA, tH;
+    tile_total_streamed<T>(projs, prs, rowbase, jm, c0, nch, L, ds, negA, tA, tH, lds);
+    publish_total(words, seq, ntiles, jm, nch, tA, tH, tag);
   }
 }
 
@@ -496,7 +502,8 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   }
   // this thread's rows: the prefixes (At, Ut) of its own rows, kept for the outputs, then the
   // tile's exclusive prefix and total
-  float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E], ta[E], th[E];
+  float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E];
+  float va[S::RG / kSeg], vh[S::RG / kSeg], tA, tH;
   {
     uint4 raw[kRPT][3];
     load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
@@ -510,9 +517,10 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
 #pragma unroll
       for (int e = 0; e < E; ++e) At[r][e] = ca[e], Ut[r][e] = ch[e];
     }
-    combine_tile<T>(ca, ch, nch, xa, xh, ta, th, &s_lds);
+    combine_total<T>(ca, ch, va, vh, tA, tH, &s_lds);
   }
-  publish_total<T>(words, seq, ntiles, tile, nch, ta, th, tag);
+  publish_total(words, seq, ntiles, tile, nch, tA, tH, tag);
+  combine_prefix<T>(va, vh, xa, xh, &s_lds);  // off the critical path: the stores are in flight
   const __amdgpu_buffer_rsrc_t wrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)words, (short)0, words_bytes, kBufferFlags);
 
