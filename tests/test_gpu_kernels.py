@@ -332,10 +332,13 @@ def test_skinny_gemm_in_place_residual(dev):
 @pytest.mark.parametrize("M,N,K,bias", [
     (300, 100, 72, True), (100, 64, 40, False), (1000, 4480, 1024, True), (257, 260, 1152, False),
     (513, 4480, 1000, True), (700, 512, 160, True), (1, 8, 8, True), (256, 256, 64, False),
+    (6000, 4480, 1024, True), (8400, 2500, 960, False), (8400, 2500, 960, True),
 ])
 def test_tiled_gemm(dev, M, N, K, bias):
     """hdcm_gemm_fwd against torch fp32 on the same bf16 operands: partial tiles in every
-    dimension (M, N not multiples of 256, K not a multiple of 64) and the bias epilogue."""
+    dimension (M, N not multiples of 256, K not a multiple of 64) and the bias epilogue; the
+    last three shapes launch more workgroups than the GPU has CUs, one of them with an odd
+    number of K steps."""
     _say("gemm", M, N, K, bias)
     g = torch.Generator().manual_seed(M + 3 * N + 7 * K)
     X = torch.randn(M, K, generator=g).to(torch.bfloat16)
