@@ -58,7 +58,7 @@ class HdcMambaLM(nn.Module):
     def forward(self, input_ids):
         _ops._on_gpu(input_ids)
         x = self.embedding(input_ids)
-        x = self.backbone(x)
+        x = self.backbone._forward(x, owned=True)  # the embedding output is this forward's own
         x = layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
         return self.lm_head(x)
 

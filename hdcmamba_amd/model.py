@@ -461,6 +461,12 @@ class HdcMamba9v3Model(nn.Module):
         self.norm_final = nn.LayerNorm(d_model)
 
     def forward(self, x):
+        return self._forward(x, owned=False)
+
+    def _forward(self, x, owned):
+        """forward; with ``owned`` (x is a temporary of the caller's, e.g. the LM's embedding
+        output) an inference forward whose rows need no padding updates x itself as the
+        residual stream instead of a copy of it."""
         _ops._on_gpu(x)
         chunks = {layer.chunk_size for layer in self.layers}
         if torch.is_grad_enabled() or len(chunks) != 1 or self.training:
@@ -473,8 +479,11 @@ class HdcMamba9v3Model(nn.Module):
             (C,) = chunks
             B, L, dm = x.shape
             pad = (C - L % C) % C
-            r = torch.empty(B, L + pad, dm, device=x.device, dtype=x.dtype)
-            r[:, pad:].copy_(x)
+            if owned and pad == 0 and x.is_contiguous():
+                r = x
+            else:
+                r = torch.empty(B, L + pad, dm, device=x.device, dtype=x.dtype)
+                r[:, pad:].copy_(x)
             for layer in self.layers:
                 if pad:
                     r[:, :pad].zero_()

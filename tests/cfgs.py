@@ -124,10 +124,15 @@ def max_rel(got, ref):
 
 
 def assert_close(got, ref, dtype, what=""):
-    """Elementwise |got-ref| <= atol + rtol*|ref| (fp32 1e-4/1e-4, bf16 2e-2/2e-2)."""
+    """Elementwise |got-ref| <= atol + rtol*|ref| (fp32 1e-4/1e-4, bf16 2e-2/2e-2) and, for bf16,
+    also the relative bound max|got-ref| <= 2e-2 max|ref|: together no looser than either
+    the elementwise or the normwise reading of "2e-2 relative"."""
     atol, rtol = tol(dtype)
     torch.testing.assert_close(got.float().cpu(), ref.float().cpu(), atol=atol, rtol=rtol,
                                msg=lambda m: f"{what}: {m}")
+    if dtype != torch.float32 and got.numel() > 0:
+        r = max_rel(got, ref)
+        assert r <= 2e-2, f"{what}: normwise max-abs/max|ref| = {r:.3e} > 2e-2"
 
 
 def assert_close_normwise(got, ref, dtype, what=""):
