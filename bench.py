@@ -532,7 +532,7 @@ def main():
         sys.stdout.write(trace_summary(args.trace_summary, args.steps, args.warmup))
         return
     if args.pmc_summary:
-        # the residual-stream copy of the embedding output: B*L*d_model bf16 values
+        # scaled by the 64 MiB calibration copy a forward run of bench.py makes first
         sys.stdout.write(pmc_summary(*args.pmc_summary, copy_bytes=COPY_CALIB_BYTES))
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))

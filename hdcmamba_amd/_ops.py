@@ -349,14 +349,14 @@ def _stats_arg(row_stats, part, rows, nparts):
 
 
 def ssm_stats_parts(d_state):
-    """Pairs per row the scan writes into row_stats (one per 64-channel block)."""
-    return -(-d_state // 64)
+    """Pairs per row the scan writes into row_stats (one per 32-channel block)."""
+    return -(-d_state // 32)
 
 
 def ssm(projs, A_log, d_state, y, h0=None, h_final=None, row_stats=None, stats_part=0):
     """Selective scan; writes y [B,L,ds] (may be a column slice of a wider buffer).  With
     ``row_stats`` ([P, B*L, 2] fp32), the sum and sum of squares of each row's stored values
-    per 64-channel block go to parts stats_part, stats_part + 1, ..."""
+    per 32-channel block go to parts stats_part, stats_part + 1, ..."""
     _on_gpu(projs, y)
     B, L, _ = projs.shape
     A_log = _same(A_log, projs, "A_log")

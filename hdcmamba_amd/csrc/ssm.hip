@@ -10,9 +10,9 @@
 //   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2).
 //
 // Forward (ssm_scan_kernel): one launch that reads every input once.  A workgroup owns a
-// tile of TR rows x 64 channels.  A thread holds 4 consecutive rows x one 16-byte channel
-// group and scans them serially in registers; the row groups' totals are folded through LDS
-// in eight segments, and the tile total (A, H) per channel is published after two barriers,
+// tile of TR = 512 rows x 32 channels.  A thread holds 8 consecutive rows x 4 channels and
+// scans them serially in registers; the row groups' totals are folded through LDS
+// in sixteen segments, and the tile total (A, H) per channel is published after two barriers,
 // before the row groups' prefixes within the tile are formed.  The workgroup then folds the
 // totals of all earlier tiles of its sequence into the
 // state entering the tile (decoupled look-back over totals, no inclusive chain), applies it
@@ -25,7 +25,7 @@
 // polls for a bounded number of rounds, then computes that tile's total itself with the
 // same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
 // whatever order the workgroups run in.  With row_stats the workgroup also writes, per row,
-// the sum and the sum of squares of the 64 values it stored (as rounded), block-major (the
+// the sum and the sum of squares of the 32 values it stored (as rounded), block-major (the
 // rows of one channel block contiguous): the partial statistics of the row LayerNorm that
 // follows, taken without another read of y.
 //
@@ -221,11 +221,11 @@ __global__ __launch_bounds__(kWave) void ssm_carry_kernel(const float* __restric
 inline int64_t ssm_tiles(int64_t L) { return (L + kTile - 1) / kTile; }
 
 // ------------------------------------------------------------- single-pass forward
-// 512 threads x 4 rows: at the 32768-row, 128-channel shape 25.8 us against 30.0 us for
-// 256 x 8 and 35.7 us for 512 x 8 (which spills), measured in isolation.
+// 512 threads x 8 rows x 4 channels: 512-row tiles of 32 channels, so a 32768-row sequence has
+// 64 tiles and every look-back is one window of lanes = tiles.
 constexpr int kScanThreads = 512;
-constexpr int kScanCh = 64;  // channels per workgroup
-constexpr int kRPT = 4;      // rows per thread
+constexpr int kScanCh = 32;  // channels per workgroup
+constexpr int kRPT = 8;      // rows per thread
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kHeaderBytes = 256;  // workspace header: epoch, finished-workgroup count
 constexpr int kDefaultSpinRounds = 256;
@@ -234,14 +234,46 @@ constexpr int kCachePolicySC1 = 16;       // buffer load cache policy: agent-sco
 
 template <typename T>
 struct ScanShape {
-  static constexpr int E = Vec<T>::N;           // channels per thread (one 16-byte group)
+  static constexpr int E = 4;                   // channels per thread (8 bytes bf16, 16 bytes fp32)
   static constexpr int CG = kScanCh / E;        // channel groups per tile
   static constexpr int RG = kScanThreads / CG;  // row groups per tile
-  static constexpr int TR = RG * kRPT;          // rows per tile: 256 (bf16), 128 (fp32)
+  static constexpr int TR = RG * kRPT;          // rows per tile: 512
 };
 
-// Largest tile count any dtype needs for L rows (the fp32 tiles are the shorter ones).
+// Largest tile count any dtype needs for L rows.
 inline int64_t scan_tiles_max(int64_t L) { return (L + ScanShape<float>::TR - 1) / ScanShape<float>::TR; }
+
+// A thread's 4 channels of one row as stored: 8 bytes (bf16) or 16 bytes (fp32).
+template <typename T> struct ScanRawOf;
+template <> struct ScanRawOf<bf16_t> { using type = uint2; };
+template <> struct ScanRawOf<float> { using type = uint4; };
+template <typename T> using ScanRaw = typename ScanRawOf<T>::type;
+template <typename T> __device__ __forceinline__ ScanRaw<T> scan_ld(const T* p) {
+  return *reinterpret_cast<const ScanRaw<T>*>(p);
+}
+__device__ __forceinline__ void scan_unpack(uint2 v, float (&o)[4]) {
+  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
+  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
+}
+__device__ __forceinline__ void scan_unpack(uint4 v, float (&o)[4]) {
+  o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y);
+  o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
+}
+// Stores 4 values (rounded to T) and adds them, as stored, and their squares to s and q.
+__device__ __forceinline__ void scan_store_sums(bf16_t* p, const float (&v)[4], float& s, float& q) {
+  const uint2 w = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  *reinterpret_cast<uint2*>(p) = w;
+  bf16_pair_sums(w.x, s, q);
+  bf16_pair_sums(w.y, s, q);
+}
+__device__ __forceinline__ void scan_store_sums(float* p, const float (&v)[4], float& s, float& q) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    s += v[e];
+    q = fmaf(v[e], v[e], q);
+  }
+}
 
 // Workspace layout: header (epoch, finished-workgroup count), then the tile totals: per
 // sequence (batch row x channel block), channel and tile one 16-byte (A, H) pair of tagged
@@ -278,26 +310,26 @@ __device__ __forceinline__ const T* row_ptr(const T* __restrict__ projs, int64_t
 // 3*kRPT loads.
 template <typename T>
 __device__ __forceinline__ void load_rows(const T* __restrict__ projs, int64_t prs, int64_t rowbase, int tile, int c0,
-                                          int nch, int L, int ds, uint4 (&raw)[kRPT][3]) {
+                                          int nch, int L, int ds, ScanRaw<T> (&raw)[kRPT][3]) {
 #pragma unroll
   for (int r = 0; r < kRPT; ++r) {
     const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
-    raw[r][0] = ldg16(p);
-    raw[r][1] = ldg16(p + ds);
-    raw[r][2] = ldg16(p + 2 * ds);
+    raw[r][0] = scan_ld<T>(p);
+    raw[r][1] = scan_ld<T>(p + ds);
+    raw[r][2] = scan_ld<T>(p + 2 * ds);
   }
 }
 
 // The pairs (a, u) of one row from its dt, x, b groups; the identity (1, 0) when !ok (rows
 // past L, channels past nch).
 template <typename T>
-__device__ __forceinline__ void pairs_of(const uint4 (&g)[3], const float (&negA)[Vec<T>::N], bool ok,
-                                         float (&a)[Vec<T>::N], float (&u)[Vec<T>::N]) {
-  constexpr int E = Vec<T>::N;
+__device__ __forceinline__ void pairs_of(const ScanRaw<T> (&g)[3], const float (&negA)[ScanShape<T>::E], bool ok,
+                                         float (&a)[ScanShape<T>::E], float (&u)[ScanShape<T>::E]) {
+  constexpr int E = ScanShape<T>::E;
   float d[E], xv[E], bv[E];
-  unpack16<T>(g[0], d);
-  unpack16<T>(g[1], xv);
-  unpack16<T>(g[2], bv);
+  scan_unpack(g[0], d);
+  scan_unpack(g[1], xv);
+  scan_unpack(g[2], bv);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const float dt = softplus20(d[e]);
@@ -311,9 +343,9 @@ __device__ __forceinline__ void pairs_of(const uint4 (&g)[3], const float (&negA
 // bits wherever it is computed (by the tile's owner, or by a workgroup computing it on the
 // owner's behalf with tile_total_streamed).
 template <typename T>
-__device__ __forceinline__ void fold_row(const uint4 (&g)[3], const float (&negA)[Vec<T>::N], bool ok,
-                                         float (&ca)[Vec<T>::N], float (&ch)[Vec<T>::N]) {
-  constexpr int E = Vec<T>::N;
+__device__ __forceinline__ void fold_row(const ScanRaw<T> (&g)[3], const float (&negA)[ScanShape<T>::E], bool ok,
+                                         float (&ca)[ScanShape<T>::E], float (&ch)[ScanShape<T>::E]) {
+  constexpr int E = ScanShape<T>::E;
   float a[E], u[E];
   pairs_of<T>(g, negA, ok, a, u);
 #pragma unroll
@@ -324,10 +356,10 @@ __device__ __forceinline__ void fold_row(const uint4 (&g)[3], const float (&negA
 }
 
 // LDS of the cross-thread part of a tile: one (A, H) pair per channel and row group, stored
-// channel-major with an odd pitch (the threads of a segment read 64 consecutive channels of
+// channel-major with an odd pitch (the threads of a segment read 32 consecutive channels of
 // one row group, and the threads of a row group write their channels, on distinct banks), and
 // the segment totals.
-constexpr int kMaxRG = kScanThreads / (kScanCh / 8);  // row groups of the bf16 tile (the most)
+constexpr int kMaxRG = kScanThreads / (kScanCh / 4);  // row groups of a tile
 constexpr int kSeg = kScanThreads / kScanCh;          // row-group segments, one thread per channel each
 constexpr int kRGPitch = kMaxRG + 1;
 struct ScanLds {
@@ -338,10 +370,10 @@ struct ScanLds {
 
 // The tile total from each thread's total (ca, ch) over its rows: the row groups' pairs go to
 // LDS, thread (segment s, channel c) folds its run of RGS row groups in order (kept in va, vh
-// for combine_prefix), and the threads of segment 0 (tid < 64, channel tid) fold the segment
+// for combine_prefix), and the threads of segment 0 (tid < 32, channel tid) fold the segment
 // totals in order into (tA, tH).  Two barriers.
 template <typename T>
-__device__ __forceinline__ void combine_total(const float (&ca)[Vec<T>::N], const float (&ch)[Vec<T>::N],
+__device__ __forceinline__ void combine_total(const float (&ca)[ScanShape<T>::E], const float (&ch)[ScanShape<T>::E],
                                               float (&va)[ScanShape<T>::RG / kSeg],
                                               float (&vh)[ScanShape<T>::RG / kSeg], float& tA, float& tH,
                                               ScanLds* lds) {
@@ -386,8 +418,8 @@ __device__ __forceinline__ void combine_total(const float (&ca)[Vec<T>::N], cons
 // back to its threads as (xa, xh) for their E channels.  Two barriers; the LDS is free after.
 template <typename T>
 __device__ __forceinline__ void combine_prefix(const float (&va)[ScanShape<T>::RG / kSeg],
-                                               const float (&vh)[ScanShape<T>::RG / kSeg], float (&xa)[Vec<T>::N],
-                                               float (&xh)[Vec<T>::N], ScanLds* lds) {
+                                               const float (&vh)[ScanShape<T>::RG / kSeg], float (&xa)[ScanShape<T>::E],
+                                               float (&xh)[ScanShape<T>::E], ScanLds* lds) {
   using S = ScanShape<T>;
   constexpr int E = S::E, CG = S::CG, RGS = S::RG / kSeg;
   const int tid = threadIdx.x;
@@ -415,13 +447,13 @@ __device__ __forceinline__ void combine_prefix(const float (&va)[ScanShape<T>::R
   __syncthreads();  // the LDS is reused
 }
 
-// A tile's total (threads tid < 64: channel tid) with the rows read one at a time (few
+// A tile's total (threads tid < 32: channel tid) with the rows read one at a time (few
 // registers in use): the kernel's own fold, row by row in the same order, then
 // combine_total, hence the same bits.
 template <typename T>
 __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs, int64_t prs, int64_t rowbase,
                                                     int tile, int c0, int nch, int L, int ds,
-                                                    const float (&negA)[Vec<T>::N], float& tA, float& tH,
+                                                    const float (&negA)[ScanShape<T>::E], float& tA, float& tH,
                                                     ScanLds* lds) {
   using S = ScanShape<T>;
   constexpr int E = S::E;
@@ -434,7 +466,7 @@ __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs,
 #pragma unroll 1
   for (int r = 0; r < kRPT; ++r) {
     const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
-    const uint4 g[3] = {ldg16(p), ldg16(p + ds), ldg16(p + 2 * ds)};
+    const ScanRaw<T> g[3] = {scan_ld<T>(p), scan_ld<T>(p + ds), scan_ld<T>(p + 2 * ds)};
     fold_row<T>(g, negA, cok && r0 + r < L, ca, ch);
   }
   float va[S::RG / kSeg], vh[S::RG / kSeg];
@@ -442,11 +474,11 @@ __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs,
   __syncthreads();  // the LDS is reused
 }
 
-// The tile total of channel tid (< 64), published for later tiles.
+// The tile total of channel tid (< 32), published for later tiles.
 __device__ __forceinline__ void publish_total(unsigned long long* words, int64_t seq, int ntiles, int tile,
                                               int nch, float tA, float tH, unsigned tag) {
   const int c = threadIdx.x;
-  if (c >= nch) return;  // also every thread past the first 64 (nch <= 64)
+  if (c >= nch) return;  // also every thread past the first 32 (nch <= 32)
   unsigned long long* p = words + 2 * ((seq * kScanCh + c) * ntiles + tile);
   __hip_atomic_store(p, pack_word(tA, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(p + 1, pack_word(tH, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -457,7 +489,7 @@ __device__ __forceinline__ void publish_total(unsigned long long* words, int64_t
 // together.
 template <typename T>
 __device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int64_t prs,
-                                                const float (&negA)[Vec<T>::N], unsigned long long* words, int64_t seq,
+                                                const float (&negA)[ScanShape<T>::E], unsigned long long* words, int64_t seq,
                                                 int64_t rowbase, int c0, int nch, int L, int ds, int ntiles, int j0,
                                                 unsigned long long missing, unsigned tag, ScanLds* lds) {
   while (missing != 0) {
@@ -469,7 +501,7 @@ __device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int
   }
 }
 
-// One workgroup per (tile, 64-channel block, sequence).  See the file header.
+// One workgroup per (tile, 32-channel block, sequence).  See the file header.
 template <typename T>
 __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     const T* __restrict__ projs, int64_t prs, const T* __restrict__ A_log, const float* __restrict__ h0,
@@ -496,7 +528,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   float negA[E];
   {
     float al[E] = {};
-    if (cok) load16<T>(A_log + c0 + cg * E, al);
+    if (cok) scan_unpack(scan_ld<T>(A_log + c0 + cg * E), al);
 #pragma unroll
     for (int e = 0; e < E; ++e) negA[e] = -fexp(al[e]);
   }
@@ -505,7 +537,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E];
   float va[S::RG / kSeg], vh[S::RG / kSeg], tA, tH;
   {
-    uint4 raw[kRPT][3];
+    ScanRaw<T> raw[kRPT][3];
     load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
     const int r0 = tile * S::TR + rg * kRPT;
     float ca[E], ch[E];
@@ -625,7 +657,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
       float v[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) v[e] = fmaf(At[r][e], hs[e], Ut[r][e]);
-      store16_sums<T>(yb + (int64_t)t * yrs, v, rsum[r], rsq[r]);
+      scan_store_sums(yb + (int64_t)t * yrs, v, rsum[r], rsq[r]);
       if (h_final != nullptr && t == L - 1) {
 #pragma unroll
         for (int e = 0; e < E; ++e) h_final[(int64_t)b * ds + c0 + cg * E + e] = v[e];
@@ -701,7 +733,7 @@ int hdcm_ssm_check_fwd(const void* projs, int64_t proj_row_stride, const void* A
   HDCM_CHECK_ARG(ds % E == 0 && proj_row_stride % E == 0 && y_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(hdcm_aligned16(projs) && hdcm_aligned16(y) && hdcm_aligned16(A_log), HDCM_EALIGN);
   HDCM_CHECK_ARG(B <= 65535 && ds <= 65535 && L < ((int64_t)1 << 30), HDCM_EUNSUPPORTED);
-  // row_stats: one (sum, sum of squares) pair per 64-channel block and row, block-major
+  // row_stats: one (sum, sum of squares) pair per 32-channel block and row, block-major
   HDCM_CHECK_ARG(!row_stats || stats_part_stride >= B * L, HDCM_EINVAL);
   HDCM_CHECK_ARG(((uintptr_t)row_stats & 7u) == 0, HDCM_EALIGN);
   // the scan kernel counts its workgroups, and addresses its tile totals, in 32 bits

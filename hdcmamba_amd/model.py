@@ -227,7 +227,7 @@ class HdcMamba9v3Block(nn.Module):
         ``normalize``) its LayerNorm in place (model.py:338-382).  x: chunk-aligned [B,L,dm].
         With ``state``, the SSM and slot states after the last row are written into it.  With
         ``row_stats`` ([P, B*L, 2] fp32) the SSM and the gate also write each row's partial
-        (sum, sum of squares): the SSM's 64-channel blocks first, then one part per head."""
+        (sum, sum of squares): the SSM's 32-channel blocks first, then one part per head."""
         B, L, dm = x.shape
         ds, H, C = self.d_state, self.num_heads, self.chunk_size
         dtype = x.dtype

@@ -103,7 +103,7 @@ int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, int64_t g_r
  * (threshold 20) and A = -exp(A_log): h_t = h_{t-1} * exp(dt*A) + dt*b*x,
  * y[b,t,:] = h_t.  h0 [B,ds] fp32 (NULL = zeros); h_final [B,ds] fp32 or NULL.
  * y rows may alias the first ds columns of the `combined` buffer.
- * row_stats (fp32, or NULL): for row r = b*L+t and 64-channel block c, the pair
+ * row_stats (fp32, or NULL): for row r = b*L+t and 32-channel block c, the pair
  * (sum, sum of squares) of the y values stored in that block (as rounded) is written to
  * row_stats[2*(c*stats_part_stride + r)] and the next float; stats_part_stride (in pairs)
  * >= B*L.  These are partial statistics for hdcm_rowln_gemm_stats_fwd.

@@ -37,8 +37,8 @@ def test_abi_version_and_strerror():
 
 def test_workspace_sizes():
     lib = _ops.lib()
-    # header + (A, H) words of 16 bytes per channel and 128-row tile
-    assert lib.hdcm_ssm_workspace_bytes(1, 32768, 128) == 256 + 128 * 256 * 16
+    # header + (A, H) words of 16 bytes per channel and 512-row tile
+    assert lib.hdcm_ssm_workspace_bytes(1, 32768, 128) == 256 + 128 * 64 * 16
     assert lib.hdcm_ssm_workspace_bytes(0, 10, 4) == 0
     n = lib.hdcm_slot_workspace_bytes(1, 32768, 1024, 16, 64, _ops.HDCM_BF16)
     assert n > 0 and n % (2 * 16 * 64 * 64 * 4) == 0

@@ -45,7 +45,7 @@ def test_noalloc_matches_workspace_entry_point(dev, dtype):
 
 def test_noalloc_rejects_inputs_beyond_its_scratch(dev):
     lib = _ops.lib()
-    B, L, ds = 64, 32768, 128  # needs 3*64*512*128*4 = 48 MiB of scratch
+    B, L, ds = 256, 32768, 128  # tile totals: 256 x 128 channels x 64 tiles x 16 B = 32 MiB of scratch
     assert lib.hdcm_ssm_workspace_bytes(B, L, ds) > (8 << 20)
     projs = torch.empty(16, dtype=torch.bfloat16, device=dev)  # never read: rejected first
     st = lib.hdcm_ssm_fwd_noalloc(projs.data_ptr(), 3 * ds, projs.data_ptr(), None, projs.data_ptr(), ds, None,
