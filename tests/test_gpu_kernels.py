@@ -68,8 +68,10 @@ def test_rowln(dev, dtype, W, affine):
 # ----------------------------------------------------------------------------- ssm
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("ds,B,L", [(64, 1, 256), (128, 2, 200), (64, 3, 1000), (32, 2, 700), (192, 1, 3000),
-                                    (128, 1, 32768)])
+                                    (40, 2, 1500), (128, 1, 32768), (64, 1, 70000)])
 def test_ssm(dev, dtype, ds, B, L):
+    """ds=40: a partial 32-channel block; L=70000: 137 tiles of 512 rows, three look-back
+    windows of 64 tiles."""
     _say("ssm", dtype, ds, B, L)
     projs, A_log = ssm_inputs(B, L, ds, dtype)
     buf = torch.zeros(B, L, ds + 16, device=dev, dtype=dtype)
@@ -85,9 +87,10 @@ def test_ssm(dev, dtype, ds, B, L):
 def test_ssm_totals_computed_for_their_owners(dev, dtype, monkeypatch):
     """With no polling budget a workgroup that finds an earlier tile's total missing computes
     it itself and publishes it for its owner; the outputs are bit-identical to the default
-    (the same code computes every total), with a start state and the final state."""
+    (the same code computes every total), with a start state and the final state.  L=40000:
+    79 tiles, so the computed totals span two look-back windows."""
     print("ssm forced fallback", dtype, flush=True)
-    ds, B, L = 128, 2, 32768
+    ds, B, L = 128, 2, 40000
     projs, A_log = ssm_inputs(B, L, ds, dtype)
     pd, ad = projs.to(dev), A_log.to(dev)
     h0 = torch.randn(B, ds, generator=torch.Generator().manual_seed(3)).to(dev)
