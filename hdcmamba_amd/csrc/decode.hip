@@ -11,10 +11,14 @@
 //   mixer_step:      SSM      h = exp(dt*A) h + dt*b*x,  y_ssm = h          (fp32 state)
 //                    slot     the weight of (t, j) is gamma^(t-j) inside t's chunk and
 //                             gamma^(t-j-1) across chunks, so with c = t mod C
-//                               S_intra <- gamma S_intra + phi(k_t)^T v_t
-//                               y_t      = phi(q_t) (S_intra + gamma^c S_prev)
-//                             and at the chunk's last token
-//                               S_prev  <- gamma^C S_prev + S_intra,  S_intra <- 0
+//                               S_eff_t = sum_{j in chunk, j<=t} gamma^(t-j) phi(k_j)^T v_j
+//                                         + gamma^c S_prev,     y_t = phi(q_t) S_eff_t,
+//                             carried as S_eff_t = S_prev + phi(k_t)^T v_t (c = 0) or
+//                             gamma S_eff_{t-1} + phi(k_t)^T v_t (c > 0), kept in S_intra
+//                             between the tokens of a chunk; at the chunk's last token
+//                               S_prev <- S_eff_t + (gamma^C - gamma^(C-1)) S_prev
+//                             (= gamma^C S_prev + the chunk's own sum).  A token reads one
+//                             fp32 state (two at a chunk's last token) and writes one.
 //                    then GroupNorm over the head's hd values and the sigmoid gate, written
 //                    next to y_ssm in the `combined` row.
 //
@@ -174,14 +178,20 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   const int cgi = tid % CG, rg = tid / CG;
   const bool act = rg < RGS;
   const int64_t sbase = (((int64_t)b * H + h) * HD) * HD + 4 * cgi;
-  // issue the state loads first
-  float4 sp[RPT], si[RPT];
+  // chunk offset: from device memory when the step runs inside a captured graph
+  const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
+  const bool first = c == 0, last = c == C - 1;
+  // issue the state loads first: the state the token builds on (S_prev at a chunk's first
+  // token, else the previous token's S_eff kept in S_intra), and S_prev again at a chunk's
+  // last token, where it is folded into the next boundary state
+  const float* zsrc = first ? S_prev : S_intra;
+  float4 sz[RPT], sp[RPT];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
     const int i = rg + RGS * k;
     if (act && i < HD) {
-      sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
-      si[k] = *reinterpret_cast<const float4*>(S_intra + sbase + (int64_t)i * HD);
+      sz[k] = *reinterpret_cast<const float4*>(zsrc + sbase + (int64_t)i * HD);
+      if (last && !first) sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
     }
   }
   // this thread's gate and GroupNorm parameters, loaded with the states (used last)
@@ -192,8 +202,6 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
     gnw_raw = gn_w[col];
     gnb_raw = gn_b[col];
   }
-  // chunk offset: from device memory when the step runs inside a captured graph
-  const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
   const float g = to_f<T>(gamma[h]);
   const float lg2 = log2f(g);
   const T* q = row + q_col + h * HD;
@@ -205,8 +213,12 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   }
   __syncthreads();
 
-  const bool first = c == 0, last = c == C - 1;
-  const float gc = fexp2((float)c * lg2), gC = fexp2((float)C * lg2);
+  // S_eff = gz * Z + phi(k)^T v with gz = 1 at a chunk's first token (Z = S_prev) and gamma
+  // after it (Z = the previous token's S_eff = S_intra + gamma^(c-1) S_prev); y = phi(q) S_eff.
+  // At the chunk's last token the boundary state gamma^C S_prev + S_intra is
+  // S_eff + (gamma^C - gamma^(C-1)) S_prev.
+  const float gz = first ? 1.0f : g;
+  const float dC = fexp2((float)C * lg2) - fexp2((float)(C - 1) * lg2);
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   if (act) {
     const float v4[4] = {sv[4 * cgi], sv[4 * cgi + 1], sv[4 * cgi + 2], sv[4 * cgi + 3]};
@@ -215,18 +227,18 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
       const int i = rg + RGS * k;
       if (i >= HD) continue;
       const float ki = sk[i], qi = sq[i];
-      float p[4] = {sp[k].x, sp[k].y, sp[k].z, sp[k].w};
-      float n[4] = {si[k].x, si[k].y, si[k].z, si[k].w};
+      const float z[4] = {sz[k].x, sz[k].y, sz[k].z, sz[k].w};
+      float n[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        n[e] = (first ? 0.f : g * n[e]) + ki * v4[e];
-        acc[e] += qi * (n[e] + gc * p[e]);
+        n[e] = fmaf(gz, z[e], ki * v4[e]);
+        acc[e] = fmaf(qi, n[e], acc[e]);
       }
       const int64_t off = sbase + (int64_t)i * HD;
       if (last) {
+        const float4 po = first ? sz[k] : sp[k];
         *reinterpret_cast<float4*>(S_prev + off) =
-            make_float4(gC * p[0] + n[0], gC * p[1] + n[1], gC * p[2] + n[2], gC * p[3] + n[3]);
-        *reinterpret_cast<float4*>(S_intra + off) = make_float4(0.f, 0.f, 0.f, 0.f);
+            make_float4(fmaf(dC, po.x, n[0]), fmaf(dC, po.y, n[1]), fmaf(dC, po.z, n[2]), fmaf(dC, po.w, n[3]));
       } else {
         *reinterpret_cast<float4*>(S_intra + off) = make_float4(n[0], n[1], n[2], n[3]);
       }

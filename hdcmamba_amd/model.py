@@ -37,7 +37,9 @@ class BlockState:
                           sequence start, whose LayerNorm is the LayerNorm bias)
     h        [B,ds]       SSM state, fp32
     S_prev   [B,H,hd,hd]  slot state at the last chunk boundary, fp32
-    S_intra  [B,H,hd,hd]  slot state of the current chunk's tokens, fp32
+    S_intra  [B,H,hd,hd]  between the tokens of a chunk, the last token's effective slot
+                          state (the chunk's own decayed sum plus gamma^c S_prev), fp32;
+                          not read at a chunk start
     pos                   offset of the next token inside its chunk
     """
     conv: torch.Tensor

@@ -257,8 +257,9 @@ int hdcm_slot_phi_chain(const void* projs, int64_t proj_row_stride, int64_t q_co
  * memory + GroupNorm + gate, reading one projs row per batch row (columns as in
  * hdcm_ssm_fwd at 0 and hdcm_slot_state_fwd at q_col).  The slot state is the pair
  * S_prev [B,H,hd,hd] (chunk-boundary state, as hdcm_slot_gate_fwd's S_final) and
- * S_intra [B,H,hd,hd] (this chunk's tokens so far; zero at a chunk start), both fp32 and
- * updated; pos = t mod C is the token's offset in its chunk (0 right after a prefill,
+ * S_intra [B,H,hd,hd] (between the tokens of a chunk: the last token's effective state,
+ * its chunk's own decayed sum plus gamma^pos S_prev; not read at a chunk start), both fp32
+ * and updated; pos = t mod C is the token's offset in its chunk (0 right after a prefill,
  * whose padded length is a multiple of C).  Writes y_ssm to columns [y_col, y_col+ds) and
  * the gated slot output to [g_col, g_col+dm) of out.  Needs hd in {32,64,96,128} and
  * 16-byte aligned S_prev / S_intra.  With pos_dev
