@@ -29,7 +29,11 @@ Parity status of each function (how it is pinned, see tests/test_oracle_*.py):
 * ``ssm_chunked``    -- pinned: equals ``ssm_sequential`` for several chunk sizes.
 * ``slot_sequential``-- pinned: hand-computed two-token KAT of the cross-chunk rule,
   C=L reduces to masked decayed attention, gamma=1 reduces to a cumulative sum.
-* ``slot_chunked``   -- pinned: equals ``slot_sequential`` (fp32) for several chunk sizes.
+* ``slot_chunked``   -- pinned: equals ``slot_sequential`` (fp32) for several chunk sizes;
+  its bf16 rounding points (phi(q), phi(k), the decayed masked scores, phi(q)*gamma^c,
+  phi(k)*gamma^(C-1-c), the carried state) against the reference's own bf16 block forward
+  (its kernels under Triton's CPU interpreter with bf16 dot operands widened to fp32): the
+  oracle matches those vectors, and leaving any one rounding point out does not.
 * ``gnorm_gate``     -- pinned: F.group_norm per token + torch.sigmoid.
 * ``rowln``          -- pinned: F.layer_norm.
 * ``block_forward_stream`` -- pinned: equals ``block_forward`` when the whole sequence is
@@ -49,7 +53,7 @@ import torch
 import torch.nn.functional as F
 
 __all__ = [
-    "BlockCfg", "kernel_rounding", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
+    "BlockCfg", "kernel_rounding", "skip_slot_rounding", "SLOT_ROUNDING_SITES", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
     "slot_sequential", "slot_chunked", "attend_sequential", "attend_chunked", "gnorm_gate", "rowln", "block_forward", "block_forward_stream",
     "model_forward", "lm_forward", "init_block_params",
 ]
@@ -96,9 +100,33 @@ class kernel_rounding:
         _KERNEL_ROUNDING = self.prev
 
 
-def _rnd(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """Kernel-side rounding of fp32 values to ``dtype``, returned as fp32 (no-op for fp32)."""
-    if dtype == torch.float32:
+# The slot recurrence's rounding points, named for the checks that leave one out to show
+# that the reference's bf16 vectors tell it apart (tests/test_oracle_reference.py).
+SLOT_ROUNDING_SITES = ("phi_q", "phi_k", "scores", "q_decay", "k_decay", "state")
+_SKIPPED_SITES: frozenset = frozenset()
+
+
+class skip_slot_rounding:
+    """Context manager that leaves the named slot rounding points out (checks only)."""
+
+    def __init__(self, *sites: str):
+        assert all(x in SLOT_ROUNDING_SITES for x in sites), sites
+        self.sites = frozenset(sites)
+
+    def __enter__(self):
+        global _SKIPPED_SITES
+        self.prev, _SKIPPED_SITES = _SKIPPED_SITES, self.sites
+        return self
+
+    def __exit__(self, *exc):
+        global _SKIPPED_SITES
+        _SKIPPED_SITES = self.prev
+
+
+def _rnd(t: torch.Tensor, dtype: torch.dtype, site: str | None = None) -> torch.Tensor:
+    """Kernel-side rounding of fp32 values to ``dtype``, returned as fp32 (no-op for fp32).
+    ``site`` names a slot rounding point that skip_slot_rounding can leave out."""
+    if dtype == torch.float32 or (site is not None and site in _SKIPPED_SITES):
         return t.float()
     if _KERNEL_ROUNDING == "trunc" and dtype == torch.bfloat16:
         return (t.float().contiguous().view(torch.int32) & ~0xFFFF).view(torch.float32)
@@ -251,8 +279,8 @@ def slot_chunked(projs, gamma, dm, ds, H, C, dtype=torch.float32, semantics="int
     q, k, v = _slot_qkv(projs, dm, ds, H)
     B, L, _, hd = q.shape
     assert L % C == 0
-    qf = _rnd(phi(q), dtype)
-    kf = _rnd(phi(k), dtype)
+    qf = _rnd(phi(q), dtype, "phi_q")
+    kf = _rnd(phi(k), dtype, "phi_k")
     if semantics == "faithful":
         blk = max(64, 1 << (hd - 1).bit_length())
         if blk > hd:
@@ -287,8 +315,8 @@ def attend_chunked(qf, kf, v, gamma, C, dtype=torch.float32, S0=None):
     assert L % C == 0
     N = L // C
     # [B,H,N,C,*]
-    qf = _rnd(qf.float(), dtype).view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
-    kf = _rnd(kf.float(), dtype).view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    qf = _rnd(qf.float(), dtype, "phi_q").view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
+    kf = _rnd(kf.float(), dtype, "phi_k").view(B, N, C, H, hk).permute(0, 3, 1, 2, 4)
     vv = v.float().view(B, N, C, H, hd).permute(0, 3, 1, 2, 4)
     lg = torch.log(gamma.float()).view(1, H, 1, 1, 1)
     idx = torch.arange(C, dtype=torch.float32)
@@ -296,18 +324,18 @@ def attend_chunked(qf, kf, v, gamma, C, dtype=torch.float32, S0=None):
     causal = diff >= 0
     decay = torch.exp(diff * lg)  # [1,H,1,C,C]
     scores = qf @ kf.transpose(-1, -2)
-    scores = _rnd(torch.where(causal, scores * decay, torch.zeros(())), dtype)
+    scores = _rnd(torch.where(causal, scores * decay, torch.zeros(())), dtype, "scores")
     y_intra = scores @ vv
     q_decay = torch.exp(idx.view(1, 1, 1, C, 1) * lg)
     k_decay = torch.exp((C - 1 - idx).view(1, 1, 1, C, 1) * lg)
-    qd = _rnd(qf * q_decay, dtype)
-    kd = _rnd(kf * k_decay, dtype)
+    qd = _rnd(qf * q_decay, dtype, "q_decay")
+    kd = _rnd(kf * k_decay, dtype, "k_decay")
     U = kd.transpose(-1, -2) @ vv  # [B,H,N,hk,hd]
     gC = torch.exp(C * lg.view(1, H, 1, 1))
     running = torch.zeros(B, H, hk, hd) if S0 is None else S0.float().clone()
     y_inter = torch.empty_like(y_intra)
     for n in range(N):
-        y_inter[:, :, n] = qd[:, :, n] @ _rnd(running, dtype)
+        y_inter[:, :, n] = qd[:, :, n] @ _rnd(running, dtype, "state")
         running = running * gC + U[:, :, n]
     y = (y_intra + y_inter).permute(0, 2, 3, 1, 4).reshape(B, L, H, hd)
     return y, running

@@ -13,6 +13,13 @@ Usage (in a container that has the reference checkout; the GPU box does not need
 The reference's CPU launch-config branch returns keys its forward never reads
 (model.py:13-14 vs 349), so each block instance gets the launch table the reference
 uses on compute capability >= 8 (model.py:17) before its forward.
+
+The interpreter keeps bf16 values as their uint16 bit patterns and its tl.dot multiplies
+those integers (values of order 1e9 for inputs of order 1).  This script widens bf16 dot
+operands to fp32 (exact) before the product, with fp32 accumulation, as a GPU's bf16 dot
+computes it; every cast the reference's kernels make stays theirs, so the bf16 block
+vectors record where the reference rounds.  The interpreter's fp32 -> bf16 cast truncates
+(a GPU rounds to nearest even); the tests compare with the oracle in that rounding mode.
 """
 from __future__ import annotations
 
@@ -31,6 +38,26 @@ def main(ref_root: str) -> None:
     import triton
 
     from hdcmamba.model import (FusedNormConv1dFunction, HdcMamba9v3Block)
+
+    import numpy as np
+    import triton.language as tl
+    from triton.runtime import interpreter as tri_interp
+
+    plain_dot = tri_interp.InterpreterBuilder.create_dot
+
+    def dot_widening_bf16(self, a, b, d, input_precision, max_num_imprecise_acc):
+        if a.dtype != tl.bfloat16 and b.dtype != tl.bfloat16:
+            return plain_dot(self, a, b, d, input_precision, max_num_imprecise_acc)
+
+        def widen(h):
+            if h.dtype == tl.bfloat16:
+                return (h.data.astype(np.uint32) << 16).view(np.float32)
+            return h.data.astype(np.float32)
+
+        acc = np.matmul(widen(a), widen(b), dtype=np.float32)
+        return tri_interp.TensorHandle(acc + d.data, d.dtype.scalar)
+
+    tri_interp.InterpreterBuilder.create_dot = dot_widening_bf16
 
     def cfg_for(blk):
         nb = lambda v, lo: max(lo, triton.next_power_of_2(v))  # noqa: E731
@@ -68,10 +95,10 @@ def main(ref_root: str) -> None:
         "block_h64_c128": (64, 16, 1, 128, 1, 256, torch.float32),
         "block_h96_c32": (96, 16, 1, 32, 1, 128, torch.float32),
         "block_h64_c64_pad": (64, 16, 1, 64, 1, 100, torch.float32),
+        # bf16 (the dots widened as above): the slot recurrence's rounding points
+        "block_h64_c64_bf16": (64, 16, 1, 64, 1, 192, torch.bfloat16),
+        "block_h32_c64_b2_bf16": (64, 16, 2, 64, 2, 128, torch.bfloat16),
     }
-    # (No bf16 block: the interpreter evaluates the slot kernel's bf16 tl.dot incorrectly,
-    # returning values of order 1e9 for inputs of order 1, so its bf16 block output says
-    # nothing about the reference on a GPU.  bf16 is covered below at kernel level.)
     for i, (name, (dm, ds, H, C, B, L, dt)) in enumerate(cases.items()):
         torch.manual_seed(100 + i)
         blk = HdcMamba9v3Block(d_model=dm, d_state=ds, num_heads=H, chunk_size=C)

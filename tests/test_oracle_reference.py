@@ -2,9 +2,11 @@
 
 tests/golden/reference_vectors.pt was written by tests/golden/make_golden.py, which ran
 N01N9/hdcmamba's constructor and forward (its Triton kernels under Triton's CPU
-interpreter).  The interpreter converts fp32 to bf16 by truncation where a GPU rounds to
-nearest even, so those comparisons run the oracle with kernel_rounding("trunc"); torch
-ops keep their usual rounding in both.
+interpreter; for the bf16 blocks its tl.dot takes bf16 operands widened to fp32, as a GPU's
+bf16 dot does, where the stock interpreter multiplies their raw bit patterns).  The
+interpreter converts fp32 to bf16 by truncation where a GPU rounds to nearest even, so
+those comparisons run the oracle with kernel_rounding("trunc"); torch ops keep their usual
+rounding in both.
 """
 from pathlib import Path
 
@@ -94,6 +96,54 @@ def test_block_faithful_matches_reference(vectors, name):
     c_ln = torch.nn.functional.layer_norm(st["combined"].float(), (ds + dm,))
     assert _rel(c_ln, v["combined_ln"]) < 2e-3
     assert _rel(y, v["y"]) < 5e-4
+
+
+BF16_BLOCKS = ["block_h64_c64_bf16", "block_h32_c64_b2_bf16"]
+
+
+def _mismatch(y, ref):
+    """(mean relative error, fraction of values that differ) of y against ref."""
+    y, ref = y.float(), ref.float()
+    d = (y - ref).abs()
+    return (d.mean() / ref.abs().mean()).item(), (d > 0).float().mean().item()
+
+
+def _bf16_block(v, skip=()):
+    dm, ds, H, C, B, L = v["args"].tolist()
+    with oracle.kernel_rounding("trunc"), oracle.skip_slot_rounding(*skip):
+        return oracle.block_forward(_params(v), v["x"], BlockCfg(dm, ds, H, C), "faithful", return_states=True)
+
+
+# The bf16 blocks below are held to: mean relative error < 3e-4 and < 8 % of the outputs
+# differing.  The faithful oracle reaches 0 / 0 % and 1.3e-4 / 3.2 % (accumulation-order
+# rounding flips); leaving out any one slot rounding point gives >= 6.1e-4 / 13.7 % on both.
+BF16_MEAN, BF16_FRAC = 3e-4, 0.08
+
+
+@pytest.mark.parametrize("name", BF16_BLOCKS)
+def test_block_bf16_matches_reference(vectors, name):
+    """bf16 blocks: the reference's forward (its kernels under the interpreter, bf16 dot
+    operands widened to fp32 as a GPU's bf16 dot takes them) against the faithful oracle
+    with the interpreter's truncating casts: equal projections, and block outputs that
+    differ only by rounding flips in a few values."""
+    v = vectors[name]
+    y, st = _bf16_block(v)
+    assert _rel(st["projs"], v["projs"]) < 1e-6
+    mean, frac = _mismatch(y, v["y"])
+    assert mean < BF16_MEAN and frac < BF16_FRAC, (mean, frac)
+    assert _rel(y, v["y"]) < 1e-2
+
+
+@pytest.mark.parametrize("site", oracle.SLOT_ROUNDING_SITES)
+def test_bf16_vectors_pin_each_slot_rounding_point(vectors, site):
+    """Each bf16 rounding point of the slot recurrence is pinned by the reference's bf16
+    block vectors: with that one point left out, the oracle falls outside the bound the
+    test above holds it to, on every bf16 block."""
+    for name in BF16_BLOCKS:
+        v = vectors[name]
+        y, _ = _bf16_block(v, (site,))
+        mean, frac = _mismatch(y, v["y"])
+        assert mean >= BF16_MEAN and frac >= BF16_FRAC, (name, site, mean, frac)
 
 
 @pytest.mark.parametrize("name", BLOCKS)
