@@ -48,8 +48,8 @@ def forward_totals(cfg, fused_out_proj=True):
     q/k/v/gate, write output), rowln (read and write combined; absent when the LayerNorm is
     folded into out_proj), out_proj (read combined, W and the residual, write the
     residual).  FLOPs: in_proj, out_proj and the slot contractions (dense C x C count).
-    Plus embedding, the two final LayerNorms and the tied head (read x and the embedding,
-    write the logits)."""
+    Plus embedding, the two final LayerNorms (norm_final, norm_f: one fused pass, read and
+    write once) and the tied head (read x and the embedding, write the logits)."""
     eb = 2
     T = cfg["B"] * cfg["L"]
     dm, ds, H, C, V = cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"], 50304
@@ -59,13 +59,13 @@ def forward_totals(cfg, fused_out_proj=True):
         + eb * (P * dm + dm * (ds + dm))
     blk_flops = 2 * T * dm * P + 2 * T * (ds + dm) * dm + T * H * (4 * C * hd + 4 * hd * hd)
     n = cfg["n_layers"]
-    tail_bytes = T * eb * dm * (1 + 4 + 1) + V * dm * eb + T * V * eb
+    tail_bytes = T * eb * dm * (1 + 2 + 1) + V * dm * eb + T * V * eb
     tail_flops = 2 * T * dm * V
     return n * blk_flops + tail_flops, n * blk_bytes + tail_bytes
 
 
 # Calls whose kernels bench.py times (hdcmamba_amd._ops wrapper names).
-KERNELS = ("norm_conv", "ssm", "slot_state", "slot_gate", "rowln", "rowln_gemm")
+KERNELS = ("norm_conv", "ssm", "slot_state", "slot_gate", "rowln", "rowln2", "rowln_gemm")
 
 
 def _mean(xs):
@@ -113,6 +113,9 @@ def kernel_table(cfg, tokens, times):
     if "rowln" in times:
         c = times["rowln"]
         out["rowln"] = hbm(_mean([k[0] for k in c]) * 1e3, 2 * dm * eb * tokens, len(c))
+    if "rowln2" in times:  # norm_final and norm_f in one pass
+        c = times["rowln2"]
+        out["rowln2"] = hbm(_mean([k[0] for k in c]) * 1e3, 2 * dm * eb * tokens, len(c))
     if "rowln_gemm" in times:
         c = times["rowln_gemm"]
         us = _mean([k[0] for k in c]) * 1e3
@@ -153,6 +156,7 @@ COPY_CALIB_BYTES = 64 << 20  # the counter runs' calibration copy (see main)
 # removed); the out_proj GEMM of the forward is the statistics variant (EPI_ROWSTATS = 2)
 KERNEL_NAMES = {"norm_conv": "norm_conv_kernel<", "ssm": "ssm_scan_kernel<", "slot_state": "slot_state_kernel<",
                 "slot_scan": "slot_scan_kernel<", "slot_gate": "slot_gate_kernel<", "rowln": "rowln_kernel<",
+                "rowln2": "rowln2_kernel<",
                 "out_proj": "gemm_bt_kernel<2,"}
 
 

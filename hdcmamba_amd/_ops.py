@@ -55,6 +55,8 @@ _PROTOS = {
                                      c_int64, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_rowln_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                c_int64, c_float, c_int, c_void_p]),
+    "hdcm_rowln2_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_float, c_void_p,
+                                c_void_p, c_float, c_int64, c_int64, c_int, c_void_p]),
     "hdcm_norm_conv_step_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float, c_int,
                                         c_void_p]),
@@ -546,6 +548,24 @@ def layer_norm(x, w=None, b=None, eps=1e-5, out=None):
         w.data_ptr() if w is not None else None, b.data_ptr() if b is not None else None,
         rows, W, float(eps), _dtype(x), _stream(x)))
     timer.end("rowln", ev)
+    return out
+
+
+def layer_norm2(x, w1, b1, eps1, w2, b2, eps2, out=None):
+    """layer_norm(layer_norm(x, w1, b1, eps1), w2, b2, eps2) in one pass, bit-identical to the
+    two calls (the intermediate rounded to x's dtype as stored); in-place when out is x."""
+    _on_gpu(x)
+    W = x.shape[-1]
+    w1, b1 = _same(w1, x, "w1"), _same(b1, x, "b1")
+    w2, b2 = _same(w2, x, "w2"), _same(b2, x, "b2")
+    if out is None:
+        out = torch.empty_like(x, memory_format=torch.contiguous_format)
+    rows = x.numel() // W if W else 0
+    ev = timer.begin("rowln2")
+    _check("hdcm_rowln2_fwd", lib().hdcm_rowln2_fwd(
+        x.data_ptr(), _rows2d(x, "x"), out.data_ptr(), _rows2d(out, "out"), w1.data_ptr(), b1.data_ptr(),
+        float(eps1), w2.data_ptr(), b2.data_ptr(), float(eps2), rows, W, _dtype(x), _stream(x)))
+    timer.end("rowln2", ev)
     return out
 
 

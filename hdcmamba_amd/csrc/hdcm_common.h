@@ -101,13 +101,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, b16x2));
 }
 
+// The 16-byte word store16 writes for these values (they, rounded to T as stored).
+template <typename T> __device__ __forceinline__ uint4 pack16(const float* in);
+template <> __device__ __forceinline__ uint4 pack16<float>(const float* in) {
+  return make_uint4(__float_as_uint(in[0]), __float_as_uint(in[1]), __float_as_uint(in[2]), __float_as_uint(in[3]));
+}
+template <> __device__ __forceinline__ uint4 pack16<bf16_t>(const float* in) {
+  return make_uint4(pack_bf16x2(in[0], in[1]), pack_bf16x2(in[2], in[3]), pack_bf16x2(in[4], in[5]),
+                    pack_bf16x2(in[6], in[7]));
+}
+
 template <> __device__ __forceinline__ void store16<bf16_t>(bf16_t* p, const float* in) {
-  uint4 v;
-  v.x = pack_bf16x2(in[0], in[1]);
-  v.y = pack_bf16x2(in[2], in[3]);
-  v.z = pack_bf16x2(in[4], in[5]);
-  v.w = pack_bf16x2(in[6], in[7]);
-  *reinterpret_cast<uint4*>(p) = v;
+  *reinterpret_cast<uint4*>(p) = pack16<bf16_t>(in);
 }
 
 // Adds a packed bf16 pair and its squares to s and q (fp32 accumulation of the exact

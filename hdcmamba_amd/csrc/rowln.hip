@@ -2,12 +2,17 @@
 //
 // Replaces F.layer_norm(combined.float(), (ds+dm,)).to(dtype) at hdcmamba/model.py:382,
 // which costs three full passes in PyTorch (upcast, normalise, downcast), and the
-// nn.LayerNorm of HdcMamba9v3Model.norm_final (model.py:400,404).
+// nn.LayerNorm of HdcMamba9v3Model.norm_final (model.py:400,404).  rowln2_kernel applies
+// two LayerNorms in one pass (the LM forward's norm_final, then the wrapper's norm_f at
+// train_fineweb.py:67,94), the intermediate rounded to the activation dtype as a stored
+// tensor would be, with the same per-row code: it equals two rowln_kernel passes bit for bit.
 //
 // One wave owns kRows rows; it issues every 128-bit load of all its rows before the
 // first reduction, so each lane keeps kRows*NG loads in flight.  Lane l owns the
 // 16-byte column groups l + 64*i.  In-place use (in == out) is safe: a wave reads all
 // of its rows before it writes any, and no two waves share a row.
+#include <type_traits>
+
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -19,6 +24,63 @@ constexpr int kRows = 4;
 // Below this many rows (decode steps: one row per sequence) every row gets its own
 // single-wave workgroup, so the rows spread over CUs instead of queueing in one wave.
 constexpr int64_t kFewRows = 4096;
+
+// LayerNorm of one row held as raw 16-byte words (lane l owns groups l + 64 i): centred
+// (two-pass) variance in fp32, then the affine; the outputs in fp32, zeros past the row.
+template <typename T, int NG, bool AFFINE>
+__device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&v)[NG][Vec<T>::N], int lane, int G,
+                                       float invW, float eps, const T* __restrict__ w, const T* __restrict__ b) {
+  constexpr int E = Vec<T>::N;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    unpack16<T>(raw[i], v[i]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) s += v[i][e];
+  }
+  const float mean = wave_total(s) * invW;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const bool ok = (lane + kWave * i) < G;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float c = ok ? v[i][e] - mean : 0.f;
+      v[i][e] = c;
+      q += c * c;
+    }
+  }
+  const float rstd = rsqrtf(wave_total(q) * invW + eps);
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = lane + kWave * i;
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[i][e] *= rstd;
+    if (AFFINE && g < G) {
+      float ww[E], bb[E];
+      load16<T>(w + g * E, ww);
+      load16<T>(b + g * E, bb);
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] = v[i][e] * ww[e] + bb[e];
+    }
+  }
+}
+
+// kRows rows of raw words of a wave, every load issued before the first reduction.
+template <typename T, int NG, int kRows>
+__device__ __forceinline__ void load_rows(const T* in, int64_t in_rs, int64_t r0, int64_t rows, int lane, int G,
+                                          uint4 (&raw)[kRows][NG]) {
+  constexpr int E = Vec<T>::N;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const int64_t row = r0 + r < rows ? r0 + r : rows - 1;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int g = lane + kWave * i;
+      raw[r][i] = g < G ? ldg16(in + row * in_rs + (int64_t)g * E) : make_uint4(0, 0, 0, 0);
+    }
+  }
+}
 
 template <typename T, int NG, bool AFFINE, int kRows, int kWavesPerBlock>
 __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
@@ -33,56 +95,52 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
   const float invW = 1.0f / (float)W;
 
   uint4 raw[kRows][NG];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const int64_t row = r0 + r < rows ? r0 + r : rows - 1;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      const int g = lane + kWave * i;
-      raw[r][i] = g < G ? ldg16(in + row * in_rs + (int64_t)g * E) : make_uint4(0, 0, 0, 0);
-    }
-  }
-
+  load_rows<T, NG, kRows>(in, in_rs, r0, rows, lane, G, raw);
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const int64_t row = r0 + r;
     float v[NG][E];
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      unpack16<T>(raw[r][i], v[i]);
-#pragma unroll
-      for (int e = 0; e < E; ++e) s += v[i][e];
-    }
-    const float mean = wave_total(s) * invW;
-    float q = 0.f;
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-      const bool ok = (lane + kWave * i) < G;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float c = ok ? v[i][e] - mean : 0.f;
-        v[i][e] = c;
-        q += c * c;
-      }
-    }
-    const float rstd = rsqrtf(wave_total(q) * invW + eps);
+    ln_row<T, NG, AFFINE>(raw[r], v, lane, G, invW, eps, w, b);
     if (row < rows) {
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
         const int g = lane + kWave * i;
-        if (g >= G) continue;
-        float o[E];
+        if (g < G) store16<T>(out + row * out_rs + (int64_t)g * E, v[i]);
+      }
+    }
+  }
+}
+
+// out = LN2(LN1(in)) with affine (w1, b1, eps1), then (w2, b2, eps2); the intermediate is
+// packed to T exactly as rowln_kernel stores it.
+template <typename T, int NG, int kRows, int kWavesPerBlock>
+__global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln2_kernel(
+    const T* in, int64_t in_rs, T* out, int64_t out_rs, const T* __restrict__ w1, const T* __restrict__ b1,
+    float eps1, const T* __restrict__ w2, const T* __restrict__ b2, float eps2, int64_t rows, int W) {
+  constexpr int E = Vec<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t r0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kRows;
+  if (r0 >= rows) return;
+  const int G = W / E;
+  const float invW = 1.0f / (float)W;
+
+  uint4 raw[kRows][NG];
+  load_rows<T, NG, kRows>(in, in_rs, r0, rows, lane, G, raw);
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] = v[i][e] * rstd;
-        if (AFFINE) {
-          float ww[E], bb[E];
-          load16<T>(w + g * E, ww);
-          load16<T>(b + g * E, bb);
+  for (int r = 0; r < kRows; ++r) {
+    const int64_t row = r0 + r;
+    float v[NG][E];
+    ln_row<T, NG, true>(raw[r], v, lane, G, invW, eps1, w1, b1);
+    uint4 mid[NG];
 #pragma unroll
-          for (int e = 0; e < E; ++e) o[e] = o[e] * ww[e] + bb[e];
-        }
-        store16<T>(out + row * out_rs + (int64_t)g * E, o);
+    for (int i = 0; i < NG; ++i) mid[i] = (lane + kWave * i) < G ? pack16<T>(v[i]) : make_uint4(0, 0, 0, 0);
+    ln_row<T, NG, true>(mid, v, lane, G, invW, eps2, w2, b2);
+    if (row < rows) {
+#pragma unroll
+      for (int i = 0; i < NG; ++i) {
+        const int g = lane + kWave * i;
+        if (g < G) store16<T>(out + row * out_rs + (int64_t)g * E, v[i]);
       }
     }
   }
@@ -113,14 +171,14 @@ int launch_ng(const void* in, int64_t in_rs, void* out, int64_t out_rs, const vo
   return hdcm_launch_status();
 }
 
-template <typename T>
-int launch(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
-           const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
-  const int G = (int)(W / Vec<T>::N);
-  const int ng = (G + kWave - 1) / kWave;
+// f(std::integral_constant<int, NG>{}) for the 16-byte groups per lane (NG <= 12) that a row
+// of W values needs.
+template <typename T, typename F>
+int with_ng(int64_t W, F&& f) {
+  const int ng = (int)((W / Vec<T>::N + kWave - 1) / kWave);
 #define HDCM_NG_CASE(n) \
   case n:               \
-    return launch_ng<T, n>(in, in_rs, out, out_rs, w, b, rows, W, eps, s);
+    return f(std::integral_constant<int, n>{});
   switch (ng) {
     HDCM_NG_CASE(1)
     HDCM_NG_CASE(2)
@@ -138,6 +196,34 @@ int launch(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void*
       return HDCM_EUNSUPPORTED;
   }
 #undef HDCM_NG_CASE
+}
+
+template <typename T>
+int launch(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
+           const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
+  return with_ng<T>(W, [&](auto ng) { return launch_ng<T, decltype(ng)::value>(in, in_rs, out, out_rs, w, b, rows, W, eps, s); });
+}
+
+template <typename T, int NG, int R, int WPB>
+void launch2_shape(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w1, const void* b1,
+                   float eps1, const void* w2, const void* b2, float eps2, int64_t rows, int64_t W, hipStream_t s) {
+  const int64_t per_block = (int64_t)WPB * R;
+  HDCM_LAUNCH((rowln2_kernel<T, NG, R, WPB>), dim3((unsigned)((rows + per_block - 1) / per_block)),
+              dim3(WPB * kWave), 0, s, (const T*)in, in_rs, (T*)out, out_rs, (const T*)w1, (const T*)b1, eps1,
+              (const T*)w2, (const T*)b2, eps2, rows, (int)W);
+}
+
+template <typename T>
+int launch2(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w1, const void* b1, float eps1,
+            const void* w2, const void* b2, float eps2, int64_t rows, int64_t W, hipStream_t s) {
+  return with_ng<T>(W, [&](auto ng) {
+    constexpr int NG = decltype(ng)::value;
+    if (rows < kFewRows)
+      launch2_shape<T, NG, 1, 1>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
+    else
+      launch2_shape<T, NG, kRows, kWavesPerBlock>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
+    return hdcm_launch_status();
+  });
 }
 
 }  // namespace
@@ -162,6 +248,29 @@ extern "C" int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out,
   if (dtype == HDCM_F32)
     return launch<float>(in, in_row_stride, out, out_row_stride, w, b, rows, width, eps, s);
   return launch<bf16_t>(in, in_row_stride, out, out_row_stride, w, b, rows, width, eps, s);
+}
+
+extern "C" int hdcm_rowln2_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out_row_stride,
+                               const void* w1, const void* b1, float eps1, const void* w2, const void* b2,
+                               float eps2, int64_t rows, int64_t width, int dtype, void* stream) {
+  HDCM_CHECK_ARG(dtype == HDCM_F32 || dtype == HDCM_BF16, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG((in && out) || rows == 0, HDCM_EINVAL);
+  HDCM_CHECK_ARG(w1 && b1 && w2 && b2, HDCM_EINVAL);
+  HDCM_CHECK_ARG(rows >= 0 && width > 0, HDCM_EINVAL);
+  const int E = 16 / hdcm_elt_size(dtype);
+  HDCM_CHECK_ARG(width % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(width / E <= 12 * kWave, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(in_row_stride >= width && out_row_stride >= width, HDCM_EINVAL);
+  HDCM_CHECK_ARG(in_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(in) && hdcm_aligned16(out), HDCM_EALIGN);
+  HDCM_CHECK_ARG(hdcm_aligned16(w1) && hdcm_aligned16(b1) && hdcm_aligned16(w2) && hdcm_aligned16(b2),
+                 HDCM_EALIGN);
+  HDCM_CHECK_ARG(rows / (kWavesPerBlock * kRows) < ((int64_t)1 << 31), HDCM_EUNSUPPORTED);
+  if (rows == 0) return HDCM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == HDCM_F32)
+    return launch2<float>(in, in_row_stride, out, out_row_stride, w1, b1, eps1, w2, b2, eps2, rows, width, s);
+  return launch2<bf16_t>(in, in_row_stride, out, out_row_stride, w1, b1, eps1, w2, b2, eps2, rows, width, s);
 }
 
 // ------------------------------------------------------------------------- backward

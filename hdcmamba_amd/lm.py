@@ -58,8 +58,8 @@ class HdcMambaLM(nn.Module):
     def forward(self, input_ids):
         _ops._on_gpu(input_ids)
         x = self.embedding(input_ids)
-        x = self.backbone._forward(x, owned=True)  # the embedding output is this forward's own
-        x = layer_norm(x, self.norm_f.weight, self.norm_f.bias, self.norm_f.eps)
+        # the embedding output is this forward's own; norm_f follows norm_final (fused in inference)
+        x = self.backbone._forward(x, owned=True, then=self.norm_f)
         return self.lm_head(x)
 
     def _logits(self, x):

@@ -465,10 +465,11 @@ class HdcMamba9v3Model(nn.Module):
     def forward(self, x):
         return self._forward(x, owned=False)
 
-    def _forward(self, x, owned):
+    def _forward(self, x, owned, then=None):
         """forward; with ``owned`` (x is a temporary of the caller's, e.g. the LM's embedding
         output) an inference forward whose rows need no padding updates x itself as the
-        residual stream instead of a copy of it."""
+        residual stream instead of a copy of it.  ``then`` (an nn.LayerNorm, the LM's norm_f)
+        is applied after norm_final, in inference as one fused pass over the rows."""
         _ops._on_gpu(x)
         chunks = {layer.chunk_size for layer in self.layers}
         if torch.is_grad_enabled() or len(chunks) != 1 or self.training:
@@ -491,7 +492,11 @@ class HdcMamba9v3Model(nn.Module):
                     r[:, :pad].zero_()
                 layer._residual_step_(r)
             x = r[:, pad:]
-        return layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
+            if then is not None:
+                nf = self.norm_final
+                return _ops.layer_norm2(x.contiguous(), nf.weight, nf.bias, nf.eps, then.weight, then.bias, then.eps)
+        x = layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
+        return x if then is None else layer_norm(x, then.weight, then.bias, then.eps)
 
     def prefill(self, x):
         """Forward over x [B,L,dm] (inference) that also returns every block's BlockState."""

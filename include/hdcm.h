@@ -352,6 +352,18 @@ int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out
                    int dtype, void* stream);
 
 /*
+ * Two affine row LayerNorms in one pass: out = LN(LN(in; w1, b1, eps1); w2, b2, eps2), the
+ * intermediate rounded to the activation dtype as a stored tensor is, by the same per-row
+ * code as hdcm_rowln_fwd, so the result equals two hdcm_rowln_fwd calls bit for bit.
+ * in and out may be the same buffer.
+ * Replaces: norm_final (hdcmamba/model.py:400,404) followed by the LM wrapper's norm_f
+ *           (train_fineweb.py:67,94) in the LM forward.
+ */
+int hdcm_rowln2_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out_row_stride,
+                    const void* w1, const void* b1, float eps1, const void* w2, const void* b2, float eps2,
+                    int64_t rows, int64_t width, int dtype, void* stream);
+
+/*
  * Gradient of hdcm_rowln_fwd: dx (x's dtype) from dy and the forward input x (the row
  * statistics are recomputed in fp32); with affine (w non-NULL) also dw = sum_rows dy*x^ and
  * db = sum_rows dy as fp32 [width], summed in a fixed order (ws: per-workgroup partials,

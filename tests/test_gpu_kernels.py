@@ -49,6 +49,30 @@ def test_norm_conv_batch_strided(dev):
 
 # ----------------------------------------------------------------------------- rowln
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,W", [(37, 320), (111, 1024), (5000, 768), (8192, 1024), (33, 2048)])
+def test_rowln2_equals_two_passes(dev, dtype, rows, W):
+    """Two affine LayerNorms in one pass (norm_final then the LM's norm_f) equal two single
+    passes bit for bit, also in place; and the oracle's two row LayerNorms within tolerance.
+    5000 and 8192 rows take the four-rows-per-wave path, the others one row per workgroup."""
+    _say("rowln2", dtype, rows, W)
+    g = torch.Generator().manual_seed(rows + W)
+    x = (3 * torch.randn(rows, W, generator=g) + 1).to(dtype)
+    p = [(1 + 0.2 * torch.randn(W, generator=g)).to(dtype), (0.3 * torch.randn(W, generator=g)).to(dtype),
+         (1 + 0.2 * torch.randn(W, generator=g)).to(dtype), (0.3 * torch.randn(W, generator=g)).to(dtype)]
+    xd = x.to(dev)
+    w1, b1, w2, b2 = [t.to(dev) for t in p]
+    two = _ops.layer_norm(_ops.layer_norm(xd, w1, b1, 1e-5), w2, b2, 1e-6)
+    one = _ops.layer_norm2(xd, w1, b1, 1e-5, w2, b2, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two)
+    _ops.layer_norm2(xd, w1, b1, 1e-5, w2, b2, 1e-6, out=xd)
+    torch.cuda.synchronize()
+    assert torch.equal(xd, two)
+    ref = oracle.rowln(oracle.rowln(x, p[0], p[1], 1e-5).to(dtype), p[2], p[3], 1e-6)
+    assert_close(one, ref, dtype, "rowln2")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("W", [320, 832, 1152, 2176])
 @pytest.mark.parametrize("affine", [False, True])
 def test_rowln(dev, dtype, W, affine):
