@@ -163,54 +163,84 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void norm_conv_kernel(
   const T* xb = x + (int64_t)blockIdx.y * x_bs;
   T* ob = out + (int64_t)blockIdx.y * o_bs;
 
-  // Prefetch ring of a full run (rows t0 .. t0+kRows-1 all exist).
   // Up to 32 columns per lane a full run takes the straight-line path; wider rows do not fit
   // its registers and go one row at a time.
   constexpr bool kFast = NG * E <= 32;
-  const bool full = kFast && t0 + kRows <= L;
-  uint4 ring[kPF][NG];
-  if (full) {
-#pragma unroll
-    for (int p = 0; p < kPF; ++p) load_row<T, NG, MASK>(ring[p], xb + (t0 + p) * x_rs, lane, G);
-  }
-
+  // Up to 16 columns per lane the raw parameters fit in registers beside the rows in flight,
+  // so every load of the prologue is issued before the first wait: the LayerNorm and conv
+  // parameters (oldest, so folding them waits for nothing else), the history rows t0-3 ..
+  // t0-1, then the prefetch ring of a full run.  Wider rows issue the ring, then load and fold
+  // the parameters, then load the history rows.
+  constexpr bool kEarly = NG * E <= 16;
+  const bool full = kFast && t0 + kRows <= L;  // rows t0 .. t0+kRows-1 all exist
   // Folded parameters: wc[k] = ln_w * conv_w[:,k], bt = ln_b * sum_k conv_w[:,k] + conv_b.
+  // prm: ln_w, ln_b, conv_b, then the 4 tap groups of conv_w ([D,4]) of a group, as stored.
   float wc[4][NG][E], bt[NG][E];
-#pragma unroll
-  for (int i = 0; i < NG; ++i) {
+  auto load_group = [&](int i, uint4 (&prm)[7]) __attribute__((always_inline)) {
     const int g = lane + kWave * i;
+    const int gs = g < G ? g : 0;  // groups past D read group 0; zeroed at the fold
+    prm[0] = ldg16(ln_w + gs * E);
+    prm[1] = ldg16(ln_b + gs * E);
+    prm[2] = ldg16(conv_b + gs * E);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) prm[3 + k] = ldg16(conv_w + (int64_t)gs * E * 4 + k * E);
+  };
+  auto fold_group = [&](int i, const uint4 (&prm)[7]) __attribute__((always_inline)) {
+    const bool ok = lane + kWave * i < G;
     float w[E], bb[E], cb[E], cw[4 * E];
-    if (g < G) {
-      load16<T>(ln_w + g * E, w);
-      load16<T>(ln_b + g * E, bb);
-      load16<T>(conv_b + g * E, cb);
+    unpack16<T>(prm[0], w);
+    unpack16<T>(prm[1], bb);
+    unpack16<T>(prm[2], cb);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) load16<T>(conv_w + (int64_t)g * E * 4 + k * E, cw + k * E);
-    } else {
-#pragma unroll
-      for (int e = 0; e < E; ++e) { w[e] = 0.f; bb[e] = 0.f; cb[e] = 0.f; }
-#pragma unroll
-      for (int e = 0; e < 4 * E; ++e) cw[e] = 0.f;
-    }
+    for (int k = 0; k < 4; ++k) unpack16<T>(prm[3 + k], cw + k * E);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       // conv_w is [D,4]: column c = g*E+e has taps cw[4e..4e+3].
-      const float c0 = cw[4 * e + 0], c1 = cw[4 * e + 1], c2 = cw[4 * e + 2], c3 = cw[4 * e + 3];
-      wc[0][i][e] = w[e] * c0;
-      wc[1][i][e] = w[e] * c1;
-      wc[2][i][e] = w[e] * c2;
-      wc[3][i][e] = w[e] * c3;
-      bt[i][e] = bb[e] * (c0 + c1 + c2 + c3) + cb[e];
+      const float c0 = ok ? cw[4 * e + 0] : 0.f, c1 = ok ? cw[4 * e + 1] : 0.f;
+      const float c2 = ok ? cw[4 * e + 2] : 0.f, c3 = ok ? cw[4 * e + 3] : 0.f;
+      const float we = ok ? w[e] : 0.f, be = ok ? bb[e] : 0.f, ce = ok ? cb[e] : 0.f;
+      wc[0][i][e] = we * c0;
+      wc[1][i][e] = we * c1;
+      wc[2][i][e] = we * c2;
+      wc[3][i][e] = we * c3;
+      bt[i][e] = be * (c0 + c1 + c2 + c3) + ce;
     }
+  };
+  uint4 hr[3][NG];
+  auto load_hist = [&]() __attribute__((always_inline)) {
+    load_row<T, NG, MASK>(hr[0], xb + (t0 >= 3 ? (t0 - 3) : 0) * x_rs, lane, G);
+    load_row<T, NG, MASK>(hr[1], xb + (t0 >= 2 ? (t0 - 2) : 0) * x_rs, lane, G);
+    load_row<T, NG, MASK>(hr[2], xb + (t0 >= 1 ? (t0 - 1) : 0) * x_rs, lane, G);
+  };
+  uint4 ring[kPF][NG];
+  auto load_ring = [&]() __attribute__((always_inline)) {
+    if (full) {
+#pragma unroll
+      for (int p = 0; p < kPF; ++p) load_row<T, NG, MASK>(ring[p], xb + (t0 + p) * x_rs, lane, G);
+    }
+  };
+  if constexpr (kEarly) {
+    uint4 prm[NG][7];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) load_group(i, prm[i]);
+    load_hist();
+    load_ring();
+#pragma unroll
+    for (int i = 0; i < NG; ++i) fold_group(i, prm[i]);
+  } else {
+    load_ring();
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      uint4 prm[7];
+      load_group(i, prm);
+      fold_group(i, prm);
+    }
+    load_hist();
   }
 
   // History rows t0-3, t0-2, t0-1 (xhat = 0 before the sequence start).
   float h3[NG][E], h2[NG][E], h1[NG][E];
   {
-    uint4 hr[3][NG];
-    load_row<T, NG, MASK>(hr[0], xb + (t0 >= 3 ? (t0 - 3) : 0) * x_rs, lane, G);
-    load_row<T, NG, MASK>(hr[1], xb + (t0 >= 2 ? (t0 - 2) : 0) * x_rs, lane, G);
-    load_row<T, NG, MASK>(hr[2], xb + (t0 >= 1 ? (t0 - 1) : 0) * x_rs, lane, G);
     float hx[3][NG][E];
     ln_rows<T, NG, 3, MASK>(hr, hx, lane, G, invD, eps);
 #pragma unroll

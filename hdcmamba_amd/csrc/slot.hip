@@ -332,8 +332,14 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, kg = lane >> 4;
   const int h = blockIdx.x, seg = blockIdx.y, b = blockIdx.z, H = gridDim.x;
-  const float lg2 = log2f(to_f<T>(gamma[h]));
-  const float ginv[4] = {1.0f, fexp2(-lg2), fexp2(-2.0f * lg2), fexp2(-3.0f * lg2)};
+  // gamma and the GroupNorm affine are loaded first and used only after the start state and
+  // the first tile have been requested, so no wait comes before those loads
+  const T gamma_raw = gamma[h];
+  T gnw_raw = T(), gnb_raw = T();
+  if constexpr (EPI) {  // every lane loads (a clamped column), so no branch holds a wait
+    gnw_raw = gn_w[h * HD + tid % HD];
+    gnb_raw = gn_b[h * HD + tid % HD];
+  }
   const bool one_chunk = cshift >= 31;  // C >= TC: every pair in a tile shares a chunk
   const int64_t rowbase = (int64_t)b * L;
   const int p_begin = seg * seg_tiles * TC;
@@ -342,11 +348,6 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   // the gate (EPI), or the chain rule's z (CHAIN: same positions as the output)
   const T* gatebase = CHAIN ? zb + out_col + h * HD : colbase + g_off;
   const int64_t grs = CHAIN ? zrs : prs;
-
-  if (EPI && tid < HD) {
-    sgw[tid] = to_f<T>(gn_w[h * HD + tid]);
-    sgb[tid] = to_f<T>(gn_b[h * HD + tid]);
-  }
 
   // Carried states: this wave owns dv tiles vt = w + 4*ov; lane holds S[dk][dv] for
   // dk = 16*mt + 4*kg + r, dv = 16*vt + l16.
@@ -401,6 +402,13 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     }
   };
   if ((EPI || CHAIN) && w < NIT) load_gate(p_begin);
+
+  const float lg2 = log2f(to_f<T>(gamma_raw));
+  const float ginv[4] = {1.0f, fexp2(-lg2), fexp2(-2.0f * lg2), fexp2(-3.0f * lg2)};
+  if (EPI && tid < HD) {  // read after the loop's first barrier
+    sgw[tid] = to_f<T>(gnw_raw);
+    sgb[tid] = to_f<T>(gnb_raw);
+  }
 
   for (int p = p_begin; p < p_end; p += TC) {
     const int tlen = min(TC, L - p);

@@ -20,7 +20,10 @@
 // agent-scope atomic words {value, tag} that bypass the non-coherent per-XCD L2s, one word
 // for A and one for H, so a reader needs no fence: a word is valid when its tag is this
 // call's.  The tag is an epoch kept in the workspace header, read by every workgroup at its
-// start and advanced by the last workgroup to finish, so the workspace never needs clearing
+// start; each workgroup then counts itself in the header (an atomic whose latency hides
+// behind its loads), and the last to arrive advances the epoch when it ends (every workgroup
+// has read the tag by then, and nothing reads the header again in this call), so the
+// workspace never needs clearing
 // (it must be zero before its first use).  A workgroup that finds an earlier total missing
 // polls for a bounded number of rounds, then computes that tile's total itself with the
 // same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
@@ -514,7 +517,6 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   __shared__ ScanLds s_lds;
   __shared__ float s_hin[kScanCh];
   __shared__ unsigned s_missing[kScanWaves][2];
-  __shared__ int s_last;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int cg = tid % CG, rg = tid / CG;
   const int tile = blockIdx.x, chb = blockIdx.y, b = blockIdx.z;
@@ -523,12 +525,29 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   const bool cok = cg * E < nch;
   const int64_t seq = (int64_t)b * gridDim.y + chb;  // this tile's sequence of totals
   const int64_t rowbase = (int64_t)b * L;
+  // Loads in this order, none waited for before the next is issued: the call's tag, this
+  // thread's A_log group, then every row of the tile; the tag and A_log (the oldest) are
+  // back before the first row, so the fold below takes the rows as they arrive.
   const unsigned tag = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  ScanRaw<T> araw{};
+  if (cok) araw = scan_ld<T>(A_log + c0 + cg * E);
+  ScanRaw<T> raw[kRPT][3];
+  load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
+  // Arrival count, issued once the tag has been read (the asm needs its value), so the last
+  // arrival knows that every workgroup of the call has read it.  The address goes through a
+  // register the compiler cannot see into, which keeps the atomic as one lane's operation
+  // whose result is waited for only at the end (not reduced across the wave on the spot).
+  unsigned arrived = 0;
+  if (tid == 0) {
+    unsigned zero;
+    __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(tag));
+    arrived = __hip_atomic_fetch_add(hdr + 1 + zero, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 
   float negA[E];
   {
-    float al[E] = {};
-    if (cok) scan_unpack(scan_ld<T>(A_log + c0 + cg * E), al);
+    float al[E];
+    scan_unpack(araw, al);
 #pragma unroll
     for (int e = 0; e < E; ++e) negA[e] = -fexp(al[e]);
   }
@@ -537,8 +556,6 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E];
   float va[S::RG / kSeg], vh[S::RG / kSeg], tA, tH;
   {
-    ScanRaw<T> raw[kRPT][3];
-    load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
     const int r0 = tile * S::TR + rg * kRPT;
     float ca[E], ch[E];
 #pragma unroll
@@ -677,14 +694,8 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     }
   }
 
-  // ---- the last workgroup to finish advances the epoch (every workgroup has read its tag and
-  // finished its look-back by then) and resets the counts for the next call
-  if (tid == 0) {
-    const unsigned total = gridDim.x * gridDim.y * gridDim.z;
-    s_last = __hip_atomic_fetch_add(hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
-  }
-  __syncthreads();
-  if (s_last && tid == 0) {
+  // ---- the last workgroup to arrive advances the epoch and resets the count for the next call
+  if (tid == 0 && arrived == gridDim.x * gridDim.y * gridDim.z - 1) {
     __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
