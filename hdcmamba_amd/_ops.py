@@ -551,6 +551,11 @@ def layer_norm(x, w=None, b=None, eps=1e-5, out=None):
     return out
 
 
+def layer_norm2_ok(x) -> bool:
+    """Whether layer_norm2 takes rows of x's width (up to 512 16-byte groups)."""
+    return x.shape[-1] * x.element_size() <= 512 * 16
+
+
 def layer_norm2(x, w1, b1, eps1, w2, b2, eps2, out=None):
     """layer_norm(layer_norm(x, w1, b1, eps1), w2, b2, eps2) in one pass, bit-identical to the
     two calls (the intermediate rounded to x's dtype as stored); in-place when out is x."""

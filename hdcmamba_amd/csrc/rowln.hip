@@ -29,7 +29,7 @@ constexpr int64_t kFewRows = 4096;
 // (two-pass) variance in fp32, then the affine; the outputs in fp32, zeros past the row.
 template <typename T, int NG, bool AFFINE>
 __device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&v)[NG][Vec<T>::N], int lane, int G,
-                                       float invW, float eps, const T* __restrict__ w, const T* __restrict__ b) {
+                                       float invW, float eps, const uint4 (&wr)[NG], const uint4 (&br)[NG]) {
   constexpr int E = Vec<T>::N;
   float s = 0.f;
 #pragma unroll
@@ -58,11 +58,25 @@ __device__ __forceinline__ void ln_row(const uint4 (&raw)[NG], float (&v)[NG][Ve
     for (int e = 0; e < E; ++e) v[i][e] *= rstd;
     if (AFFINE && g < G) {
       float ww[E], bb[E];
-      load16<T>(w + g * E, ww);
-      load16<T>(b + g * E, bb);
+      unpack16<T>(wr[i], ww);
+      unpack16<T>(br[i], bb);
 #pragma unroll
       for (int e = 0; e < E; ++e) v[i][e] = v[i][e] * ww[e] + bb[e];
     }
+  }
+}
+
+// The affine's weight and bias groups of this lane, as stored (loaded with the rows, so no
+// load waits behind a row's reductions).
+template <typename T, int NG>
+__device__ __forceinline__ void load_affine(const T* __restrict__ w, const T* __restrict__ b, int lane, int G,
+                                            uint4 (&wr)[NG], uint4 (&br)[NG]) {
+  constexpr int E = Vec<T>::N;
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    const int g = lane + kWave * i;
+    wr[i] = g < G ? ldg16(w + g * E) : make_uint4(0, 0, 0, 0);
+    br[i] = g < G ? ldg16(b + g * E) : make_uint4(0, 0, 0, 0);
   }
 }
 
@@ -96,11 +110,13 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
 
   uint4 raw[kRows][NG];
   load_rows<T, NG, kRows>(in, in_rs, r0, rows, lane, G, raw);
+  uint4 wr[NG], br[NG];
+  if constexpr (AFFINE) load_affine<T, NG>(w, b, lane, G, wr, br);
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const int64_t row = r0 + r;
     float v[NG][E];
-    ln_row<T, NG, AFFINE>(raw[r], v, lane, G, invW, eps, w, b);
+    ln_row<T, NG, AFFINE>(raw[r], v, lane, G, invW, eps, wr, br);
     if (row < rows) {
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
@@ -110,6 +126,10 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln_kernel(
     }
   }
 }
+
+// Widest row of rowln2_kernel in 16-byte groups per lane: its registers hold the rows and both
+// affines (8 groups: 4096 bf16 or 2048 fp32 columns).
+constexpr int kRowln2MaxNG = 8;
 
 // out = LN2(LN1(in)) with affine (w1, b1, eps1), then (w2, b2, eps2); the intermediate is
 // packed to T exactly as rowln_kernel stores it.
@@ -127,15 +147,19 @@ __global__ __launch_bounds__(kWavesPerBlock* kWave) void rowln2_kernel(
 
   uint4 raw[kRows][NG];
   load_rows<T, NG, kRows>(in, in_rs, r0, rows, lane, G, raw);
+  // both affines ride with the rows (up to 8 groups per lane, kRowln2MaxNG)
+  uint4 w1r[NG], b1r[NG], w2r[NG], b2r[NG];
+  load_affine<T, NG>(w1, b1, lane, G, w1r, b1r);
+  load_affine<T, NG>(w2, b2, lane, G, w2r, b2r);
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const int64_t row = r0 + r;
     float v[NG][E];
-    ln_row<T, NG, true>(raw[r], v, lane, G, invW, eps1, w1, b1);
+    ln_row<T, NG, true>(raw[r], v, lane, G, invW, eps1, w1r, b1r);
     uint4 mid[NG];
 #pragma unroll
     for (int i = 0; i < NG; ++i) mid[i] = (lane + kWave * i) < G ? pack16<T>(v[i]) : make_uint4(0, 0, 0, 0);
-    ln_row<T, NG, true>(mid, v, lane, G, invW, eps2, w2, b2);
+    ln_row<T, NG, true>(mid, v, lane, G, invW, eps2, w2r, b2r);
     if (row < rows) {
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
@@ -171,14 +195,15 @@ int launch_ng(const void* in, int64_t in_rs, void* out, int64_t out_rs, const vo
   return hdcm_launch_status();
 }
 
-// f(std::integral_constant<int, NG>{}) for the 16-byte groups per lane (NG <= 12) that a row
-// of W values needs.
-template <typename T, typename F>
+// f(std::integral_constant<int, NG>{}) for the 16-byte groups per lane (NG <= MaxNG <= 12) that
+// a row of W values needs.
+template <typename T, int MaxNG, typename F>
 int with_ng(int64_t W, F&& f) {
   const int ng = (int)((W / Vec<T>::N + kWave - 1) / kWave);
-#define HDCM_NG_CASE(n) \
-  case n:               \
-    return f(std::integral_constant<int, n>{});
+#define HDCM_NG_CASE(n)                                                       \
+  case n:                                                                     \
+    if constexpr (n <= MaxNG) return f(std::integral_constant<int, n>{}); \
+    return HDCM_EUNSUPPORTED;
   switch (ng) {
     HDCM_NG_CASE(1)
     HDCM_NG_CASE(2)
@@ -201,7 +226,7 @@ int with_ng(int64_t W, F&& f) {
 template <typename T>
 int launch(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w,
            const void* b, int64_t rows, int64_t W, float eps, hipStream_t s) {
-  return with_ng<T>(W, [&](auto ng) { return launch_ng<T, decltype(ng)::value>(in, in_rs, out, out_rs, w, b, rows, W, eps, s); });
+  return with_ng<T, 12>(W, [&](auto ng) { return launch_ng<T, decltype(ng)::value>(in, in_rs, out, out_rs, w, b, rows, W, eps, s); });
 }
 
 template <typename T, int NG, int R, int WPB>
@@ -216,7 +241,7 @@ void launch2_shape(const void* in, int64_t in_rs, void* out, int64_t out_rs, con
 template <typename T>
 int launch2(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void* w1, const void* b1, float eps1,
             const void* w2, const void* b2, float eps2, int64_t rows, int64_t W, hipStream_t s) {
-  return with_ng<T>(W, [&](auto ng) {
+  return with_ng<T, kRowln2MaxNG>(W, [&](auto ng) {
     constexpr int NG = decltype(ng)::value;
     if (rows < kFewRows)
       launch2_shape<T, NG, 1, 1>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
@@ -259,7 +284,7 @@ extern "C" int hdcm_rowln2_fwd(const void* in, int64_t in_row_stride, void* out,
   HDCM_CHECK_ARG(rows >= 0 && width > 0, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(width % E == 0, HDCM_EALIGN);
-  HDCM_CHECK_ARG(width / E <= 12 * kWave, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(width / E <= kRowln2MaxNG * kWave, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(in_row_stride >= width && out_row_stride >= width, HDCM_EINVAL);
   HDCM_CHECK_ARG(in_row_stride % E == 0 && out_row_stride % E == 0, HDCM_EALIGN);
   HDCM_CHECK_ARG(hdcm_aligned16(in) && hdcm_aligned16(out), HDCM_EALIGN);

@@ -783,26 +783,36 @@ __global__ __launch_bounds__(kThreads) void slot_scan_kernel(const float* __rest
   const int e = blockIdx.x * kThreads + threadIdx.x;
   const int h = blockIdx.y, b = blockIdx.z, H = gridDim.y;
   if (e >= HD2) return;
-  const float gs = fexp2((float)seg_len * log2f(to_f<T>(gamma[h])));
   const int64_t bh = (int64_t)b * H + h;
-  float a = S0 ? S0[bh * HD2 + e] : 0.f;
+  const T graw = gamma[h];
   const float* u = U + bh * nseg * HD2 + e;
   float* o = Ain + bh * nseg * HD2 + e;
-  constexpr int kU = 32;  // loads of a batch are all in flight before the recurrence uses them
-  int s = 0;
-  for (; s + kU <= nseg; s += kU) {
-    float uu[kU];
+  // Segments in batches of kU whose loads are all in flight before the recurrence uses them.
+  // The first batch is straight-line code issued before S0 is loaded and gamma used, so no
+  // wait precedes its loads; U[s] is needed only for s + 1 < nseg.
+  constexpr int kU = 32;
+  float uu[kU];
+#pragma unroll
+  for (int k = 0; k < kU; ++k) uu[k] = (k + 1 < nseg) ? u[(int64_t)k * HD2] : 0.f;
+  float a = S0 ? S0[bh * HD2 + e] : 0.f;
+  const float gs = fexp2((float)seg_len * log2f(to_f<T>(graw)));
+#pragma unroll
+  for (int k = 0; k < kU; ++k) {
+    if (k < nseg) {
+      o[(int64_t)k * HD2] = a;
+      a = a * gs + uu[k];
+    }
+  }
+  for (int s = kU; s < nseg; s += kU) {
 #pragma unroll
     for (int k = 0; k < kU; ++k) uu[k] = (s + k + 1 < nseg) ? u[(int64_t)(s + k) * HD2] : 0.f;
 #pragma unroll
     for (int k = 0; k < kU; ++k) {
-      o[(int64_t)(s + k) * HD2] = a;
-      a = a * gs + uu[k];
+      if (s + k < nseg) {
+        o[(int64_t)(s + k) * HD2] = a;
+        a = a * gs + uu[k];
+      }
     }
-  }
-  for (; s < nseg; ++s) {
-    o[(int64_t)s * HD2] = a;
-    if (s + 1 < nseg) a = a * gs + u[(int64_t)s * HD2];
   }
 }
 

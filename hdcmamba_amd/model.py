@@ -492,7 +492,7 @@ class HdcMamba9v3Model(nn.Module):
                     r[:, :pad].zero_()
                 layer._residual_step_(r)
             x = r[:, pad:]
-            if then is not None:
+            if then is not None and _ops.layer_norm2_ok(x):
                 nf = self.norm_final
                 return _ops.layer_norm2(x.contiguous(), nf.weight, nf.bias, nf.eps, then.weight, then.bias, then.eps)
         x = layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)

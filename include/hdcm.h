@@ -355,7 +355,8 @@ int hdcm_rowln_fwd(const void* in, int64_t in_row_stride, void* out, int64_t out
  * Two affine row LayerNorms in one pass: out = LN(LN(in; w1, b1, eps1); w2, b2, eps2), the
  * intermediate rounded to the activation dtype as a stored tensor is, by the same per-row
  * code as hdcm_rowln_fwd, so the result equals two hdcm_rowln_fwd calls bit for bit.
- * in and out may be the same buffer.
+ * in and out may be the same buffer.  width up to 512 16-byte groups (4096 bf16 or 2048 fp32
+ * columns), HDCM_EUNSUPPORTED beyond.
  * Replaces: norm_final (hdcmamba/model.py:400,404) followed by the LM wrapper's norm_f
  *           (train_fineweb.py:67,94) in the LM forward.
  */

@@ -72,6 +72,15 @@ def test_rowln2_equals_two_passes(dev, dtype, rows, W):
     assert_close(one, ref, dtype, "rowln2")
 
 
+def test_rowln2_rejects_rows_past_its_width(dev):
+    """Rows wider than 512 16-byte groups are refused (the model runs two passes there)."""
+    x = torch.zeros(4, 4104, device=dev, dtype=torch.bfloat16)
+    w = torch.ones(4104, device=dev, dtype=torch.bfloat16)
+    assert not _ops.layer_norm2_ok(x) and _ops.layer_norm2_ok(x[:, :4096])
+    with pytest.raises(RuntimeError):
+        _ops.layer_norm2(x, w, w, 1e-5, w, w, 1e-5)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("W", [320, 832, 1152, 2176])
 @pytest.mark.parametrize("affine", [False, True])
