@@ -18,7 +18,7 @@
 //                             between the tokens of a chunk; at the chunk's last token
 //                               S_prev <- S_eff_t + (gamma^C - gamma^(C-1)) S_prev
 //                             (= gamma^C S_prev + the chunk's own sum).  A token reads one
-//                             fp32 state (two at a chunk's last token) and writes one.
+//                             fp32 state (two at a chunk's first and last token) and writes one.
 //                    then GroupNorm over the head's hd values and the sigmoid gate, written
 //                    next to y_ssm in the `combined` row.
 //
@@ -180,18 +180,23 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   const int64_t sbase = (((int64_t)b * H + h) * HD) * HD + 4 * cgi;
   // chunk offset: from device memory when the step runs inside a captured graph
   const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
-  const bool first = c == 0, last = c == C - 1;
-  // issue the state loads first: the state the token builds on (S_prev at a chunk's first
-  // token, else the previous token's S_eff kept in S_intra), and S_prev again at a chunk's
-  // last token, where it is folded into the next boundary state
-  const float* zsrc = first ? S_prev : S_intra;
+  // The state the token builds on: the previous token's S_eff kept in S_intra, loaded while
+  // the offset is still in flight (right for every token but a chunk's first), or S_prev at a
+  // chunk's first token; S_prev again at a chunk's last token, where it is folded into the
+  // next boundary state.
   float4 sz[RPT], sp[RPT];
 #pragma unroll
   for (int k = 0; k < RPT; ++k) {
     const int i = rg + RGS * k;
+    if (act && i < HD) sz[k] = *reinterpret_cast<const float4*>(S_intra + sbase + (int64_t)i * HD);
+  }
+  const bool first = c == 0, last = c == C - 1;
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int i = rg + RGS * k;
     if (act && i < HD) {
-      sz[k] = *reinterpret_cast<const float4*>(zsrc + sbase + (int64_t)i * HD);
-      if (last && !first) sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
+      if (first) sz[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
+      else if (last) sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
     }
   }
   // this thread's gate and GroupNorm parameters, loaded with the states (used last)
