@@ -10,7 +10,8 @@
 //   (a1, u1) then (a2, u2)  =  (a1*a2, a2*u1 + u2).
 //
 // Forward (ssm_scan_kernel): one launch that reads every input once.  A workgroup owns a
-// tile of TR = 512 rows x 32 channels.  A thread holds 8 consecutive rows x 4 channels and
+// tile of TR = 512 rows x 32 channels.  A thread holds one 16-byte channel group (8 bf16 or
+// 4 fp32 channels) of 4 (bf16) or 8 (fp32) consecutive rows and
 // scans them serially in registers; the row groups' totals are folded through LDS
 // in sixteen segments, and the tile total (A, H) per channel is published after two barriers,
 // before the row groups' prefixes within the tile are formed.  The workgroup then folds the
@@ -224,11 +225,11 @@ __global__ __launch_bounds__(kWave) void ssm_carry_kernel(const float* __restric
 inline int64_t ssm_tiles(int64_t L) { return (L + kTile - 1) / kTile; }
 
 // ------------------------------------------------------------- single-pass forward
-// 512 threads x 8 rows x 4 channels: 512-row tiles of 32 channels, so a 32768-row sequence has
+// 512 threads x (4 rows x 8 channels bf16, 8 rows x 4 channels fp32): 512-row tiles of 32
+// channels, so a 32768-row sequence has
 // 64 tiles and every look-back is one window of lanes = tiles.
 constexpr int kScanThreads = 512;
 constexpr int kScanCh = 32;  // channels per workgroup
-constexpr int kRPT = 8;      // rows per thread
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kHeaderBytes = 256;  // workspace header: epoch, finished-workgroup count
 constexpr int kDefaultSpinRounds = 256;
@@ -237,45 +238,27 @@ constexpr int kCachePolicySC1 = 16;       // buffer load cache policy: agent-sco
 
 template <typename T>
 struct ScanShape {
-  static constexpr int E = 4;                   // channels per thread (8 bytes bf16, 16 bytes fp32)
+  static constexpr int E = 16 / sizeof(T);      // channels per thread: one 16-byte group
+  static constexpr int RPT = 32 / E;            // rows per thread (4 bf16, 8 fp32)
   static constexpr int CG = kScanCh / E;        // channel groups per tile
   static constexpr int RG = kScanThreads / CG;  // row groups per tile
-  static constexpr int TR = RG * kRPT;          // rows per tile: 512
+  static constexpr int TR = RG * RPT;           // rows per tile: 512
 };
 
 // Largest tile count any dtype needs for L rows.
 inline int64_t scan_tiles_max(int64_t L) { return (L + ScanShape<float>::TR - 1) / ScanShape<float>::TR; }
 
-// A thread's 4 channels of one row as stored: 8 bytes (bf16) or 16 bytes (fp32).
+// A thread's channels of one row as stored: one 16-byte group.
 template <typename T> struct ScanRawOf;
-template <> struct ScanRawOf<bf16_t> { using type = uint2; };
+template <> struct ScanRawOf<bf16_t> { using type = uint4; };
 template <> struct ScanRawOf<float> { using type = uint4; };
 template <typename T> using ScanRaw = typename ScanRawOf<T>::type;
 template <typename T> __device__ __forceinline__ ScanRaw<T> scan_ld(const T* p) {
   return *reinterpret_cast<const ScanRaw<T>*>(p);
 }
-__device__ __forceinline__ void scan_unpack(uint2 v, float (&o)[4]) {
-  o[0] = __uint_as_float(v.x << 16); o[1] = __uint_as_float(v.x & 0xffff0000u);
-  o[2] = __uint_as_float(v.y << 16); o[3] = __uint_as_float(v.y & 0xffff0000u);
-}
-__device__ __forceinline__ void scan_unpack(uint4 v, float (&o)[4]) {
-  o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y);
-  o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
-}
-// Stores 4 values (rounded to T) and adds them, as stored, and their squares to s and q.
-__device__ __forceinline__ void scan_store_sums(bf16_t* p, const float (&v)[4], float& s, float& q) {
-  const uint2 w = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-  *reinterpret_cast<uint2*>(p) = w;
-  bf16_pair_sums(w.x, s, q);
-  bf16_pair_sums(w.y, s, q);
-}
-__device__ __forceinline__ void scan_store_sums(float* p, const float (&v)[4], float& s, float& q) {
-  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    s += v[e];
-    q = fmaf(v[e], v[e], q);
-  }
+template <typename T>
+__device__ __forceinline__ void scan_unpack(ScanRaw<T> v, float (&o)[ScanShape<T>::E]) {
+  unpack16<T>(v, o);
 }
 
 // Workspace layout: header (epoch, finished-workgroup count), then the tile totals: per
@@ -298,24 +281,24 @@ __device__ __forceinline__ unsigned long long pack_word(float v, unsigned tag) {
 __device__ __forceinline__ float word_value(unsigned long long w) { return __uint_as_float((unsigned)w); }
 __device__ __forceinline__ unsigned word_tag(unsigned long long w) { return (unsigned)(w >> 32); }
 
-// Row r (< kRPT) of this thread's rows of a tile (tile*TR + rg*kRPT + r, clamped to L-1:
+// Row r (< RPT) of this thread's rows of a tile (tile*TR + rg*RPT + r, clamped to L-1:
 // rows past L are re-read and masked later) at its channel group (group 0 past nch).
 template <typename T>
 __device__ __forceinline__ const T* row_ptr(const T* __restrict__ projs, int64_t prs, int64_t rowbase, int tile,
                                             int c0, int nch, int L, int r) {
   using S = ScanShape<T>;
   const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
-  const int t = min(tile * S::TR + rg * kRPT + r, L - 1);
+  const int t = min(tile * S::TR + rg * ScanShape<T>::RPT + r, L - 1);
   return projs + (rowbase + t) * prs + (cg * S::E < nch ? c0 + cg * S::E : 0);
 }
 
 // This thread's rows x E channels of dt, x, b, as stored: every thread issues the same
-// 3*kRPT loads.
+// 3*RPT loads.
 template <typename T>
 __device__ __forceinline__ void load_rows(const T* __restrict__ projs, int64_t prs, int64_t rowbase, int tile, int c0,
-                                          int nch, int L, int ds, ScanRaw<T> (&raw)[kRPT][3]) {
+                                          int nch, int L, int ds, ScanRaw<T> (&raw)[ScanShape<T>::RPT][3]) {
 #pragma unroll
-  for (int r = 0; r < kRPT; ++r) {
+  for (int r = 0; r < ScanShape<T>::RPT; ++r) {
     const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
     raw[r][0] = scan_ld<T>(p);
     raw[r][1] = scan_ld<T>(p + ds);
@@ -330,9 +313,9 @@ __device__ __forceinline__ void pairs_of(const ScanRaw<T> (&g)[3], const float (
                                          float (&a)[ScanShape<T>::E], float (&u)[ScanShape<T>::E]) {
   constexpr int E = ScanShape<T>::E;
   float d[E], xv[E], bv[E];
-  scan_unpack(g[0], d);
-  scan_unpack(g[1], xv);
-  scan_unpack(g[2], bv);
+  scan_unpack<T>(g[0], d);
+  scan_unpack<T>(g[1], xv);
+  scan_unpack<T>(g[2], bv);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const float dt = softplus20(d[e]);
@@ -362,7 +345,7 @@ __device__ __forceinline__ void fold_row(const ScanRaw<T> (&g)[3], const float (
 // channel-major with an odd pitch (the threads of a segment read 32 consecutive channels of
 // one row group, and the threads of a row group write their channels, on distinct banks), and
 // the segment totals.
-constexpr int kMaxRG = kScanThreads / (kScanCh / 4);  // row groups of a tile
+constexpr int kMaxRG = kScanThreads / (kScanCh / 8);  // row groups of a tile (bf16: the most)
 constexpr int kSeg = kScanThreads / kScanCh;          // row-group segments, one thread per channel each
 constexpr int kRGPitch = kMaxRG + 1;
 struct ScanLds {
@@ -462,12 +445,12 @@ __device__ __forceinline__ void tile_total_streamed(const T* __restrict__ projs,
   constexpr int E = S::E;
   const int tid = threadIdx.x, cg = tid % S::CG, rg = tid / S::CG;
   const bool cok = cg * E < nch;
-  const int r0 = tile * S::TR + rg * kRPT;
+  const int r0 = tile * S::TR + rg * ScanShape<T>::RPT;
   float ca[E], ch[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) ca[e] = 1.f, ch[e] = 0.f;
 #pragma unroll 1
-  for (int r = 0; r < kRPT; ++r) {
+  for (int r = 0; r < ScanShape<T>::RPT; ++r) {
     const T* p = row_ptr<T>(projs, prs, rowbase, tile, c0, nch, L, r);
     const ScanRaw<T> g[3] = {scan_ld<T>(p), scan_ld<T>(p + ds), scan_ld<T>(p + 2 * ds)};
     fold_row<T>(g, negA, cok && r0 + r < L, ca, ch);
@@ -531,7 +514,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   const unsigned tag = __hip_atomic_load(hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   ScanRaw<T> araw{};
   if (cok) araw = scan_ld<T>(A_log + c0 + cg * E);
-  ScanRaw<T> raw[kRPT][3];
+  ScanRaw<T> raw[ScanShape<T>::RPT][3];
   load_rows<T>(projs, prs, rowbase, tile, c0, nch, L, ds, raw);
   // Arrival count, issued once the tag has been read (the asm needs its value), so the last
   // arrival knows that every workgroup of the call has read it.  The address goes through a
@@ -547,21 +530,21 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   float negA[E];
   {
     float al[E];
-    scan_unpack(araw, al);
+    scan_unpack<T>(araw, al);
 #pragma unroll
     for (int e = 0; e < E; ++e) negA[e] = -fexp(al[e]);
   }
   // this thread's rows: the prefixes (At, Ut) of its own rows, kept for the outputs, then the
   // tile's exclusive prefix and total
-  float At[kRPT][E], Ut[kRPT][E], xa[E], xh[E];
+  float At[S::RPT][E], Ut[S::RPT][E], xa[E], xh[E];
   float va[S::RG / kSeg], vh[S::RG / kSeg], tA, tH;
   {
-    const int r0 = tile * S::TR + rg * kRPT;
+    const int r0 = tile * S::TR + rg * ScanShape<T>::RPT;
     float ca[E], ch[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) ca[e] = 1.f, ch[e] = 0.f;
 #pragma unroll
-    for (int r = 0; r < kRPT; ++r) {
+    for (int r = 0; r < ScanShape<T>::RPT; ++r) {
       fold_row<T>(raw[r], negA, cok && r0 + r < L, ca, ch);
 #pragma unroll
       for (int e = 0; e < E; ++e) At[r][e] = ca[e], Ut[r][e] = ch[e];
@@ -659,22 +642,22 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   __syncthreads();
 
   // ---- outputs: y_t = U_t + A_t * (state entering this thread's rows)
-  const int r0 = tile * S::TR + rg * kRPT;
+  const int r0 = tile * S::TR + rg * ScanShape<T>::RPT;
   float hs[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) hs[e] = fmaf(xa[e], s_hin[cg * E + e], xh[e]);
-  float rsum[kRPT], rsq[kRPT];  // this thread's part of each row's sum and sum of squares
+  float rsum[S::RPT], rsq[S::RPT];  // this thread's part of each row's sum and sum of squares
   if (cok) {
     T* yb = y + rowbase * yrs + c0 + cg * E;
 #pragma unroll
-    for (int r = 0; r < kRPT; ++r) {
+    for (int r = 0; r < ScanShape<T>::RPT; ++r) {
       const int t = r0 + r;
       rsum[r] = rsq[r] = 0.f;
       if (t >= L) continue;
       float v[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) v[e] = fmaf(At[r][e], hs[e], Ut[r][e]);
-      scan_store_sums(yb + (int64_t)t * yrs, v, rsum[r], rsq[r]);
+      store16_sums<T>(yb + (int64_t)t * yrs, v, rsum[r], rsq[r]);
       if (h_final != nullptr && t == L - 1) {
 #pragma unroll
         for (int e = 0; e < E; ++e) h_final[(int64_t)b * ds + c0 + cg * E + e] = v[e];
@@ -682,11 +665,11 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     }
   } else {
 #pragma unroll
-    for (int r = 0; r < kRPT; ++r) rsum[r] = rsq[r] = 0.f;
+    for (int r = 0; r < ScanShape<T>::RPT; ++r) rsum[r] = rsq[r] = 0.f;
   }
   if (row_stats != nullptr) {  // the CG threads of a row group are consecutive lanes
 #pragma unroll
-    for (int r = 0; r < kRPT; ++r) {
+    for (int r = 0; r < ScanShape<T>::RPT; ++r) {
       const float s = group_sum<CG>(rsum[r]), q = group_sum<CG>(rsq[r]);
       const int t = r0 + r;
       if (cg == 0 && t < L)
