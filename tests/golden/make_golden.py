@@ -7,7 +7,7 @@ inputs, and saves inputs, weights, captured intermediates and outputs as plain t
 files (torch.save of dicts of tensors; load with weights_only=True).  Nothing of the
 reference's code is copied into the fixtures: they hold data only.
 
-Usage (in a container that has the reference checkout; the GPU box does not need it):
+Usage (where the reference checkout is present; running the tests does not need it):
     python tests/golden/make_golden.py /path/to/reference
 
 The reference's CPU launch-config branch returns keys its forward never reads
