@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libhdcmamba_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 HDCM_F32, HDCM_BF16 = 0, 1
 _DTYPES = {torch.float32: HDCM_F32, torch.bfloat16: HDCM_BF16}
@@ -25,6 +25,8 @@ _PROTOS = {
     "hdcm_strerror": (ctypes.c_char_p, [c_int]),
     "hdcm_time_launches": (c_int, [c_void_p, c_void_p, c_int]),
     "hdcm_timed_launch_count": (c_int, []),
+    "hdcm_set_option": (c_int, [c_int, c_int]),
+    "hdcm_get_option": (c_int, [c_int]),
     "hdcm_norm_conv_fwd": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_float,
                                    c_int, c_void_p]),
@@ -264,6 +266,30 @@ class _Timer:
 
 
 timer = _Timer()
+
+# launch options of the library (hdcm_set_option)
+OPTIONS = {"ssm_spin_rounds": 1, "slot_seg_tiles": 2}
+
+
+class option:
+    """Context manager that sets a library launch option and restores its previous value:
+    ``with _ops.option("slot_seg_tiles", 8): ...``.  ssm_spin_rounds = polling rounds of the
+    scan's look-back before it computes a missing total itself (0 forces that path);
+    slot_seg_tiles = row tiles per slot segment (0 = automatic).  Launches read the value
+    current when they are issued (a recorded graph keeps the value of its capture)."""
+
+    def __init__(self, name, value):
+        self.key = OPTIONS[name]
+        self.value = int(value)
+
+    def __enter__(self):
+        self.old = lib().hdcm_get_option(self.key)
+        _check("hdcm_set_option", lib().hdcm_set_option(self.key, self.value))
+        return self
+
+    def __exit__(self, *exc):
+        _check("hdcm_set_option", lib().hdcm_set_option(self.key, self.old))
+        return False
 
 
 # ----------------------------------------------------------------------------- wrappers

@@ -23,6 +23,10 @@ struct HdcmTiming {
 };
 extern thread_local HdcmTiming hdcm_timing_slot;
 
+// Launch options (hdcm_set_option, api.hip): their values when the library loaded come from
+// the environment, read once; a launch reads the value current when it is issued.
+int hdcm_option_value(int option);
+
 #define HDCM_LAUNCH(kernel, grid, block, shmem, stream, ...)                                      \
   do {                                                                                            \
     if (hdcm_timing_slot.used < hdcm_timing_slot.n) {                                             \

@@ -821,13 +821,6 @@ struct SlotPlan {
   bool has_w;
 };
 
-int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  if (!v || !*v) return dflt;
-  const int x = atoi(v);
-  return x > 0 ? x : dflt;
-}
-
 int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype, SlotPlan* pl) {
   if (dtype != HDCM_F32 && dtype != HDCM_BF16) return HDCM_EUNSUPPORTED;
   if (B < 0 || L < 0 || dm <= 0 || H <= 0 || C <= 0 || dm % H) return HDCM_EINVAL;
@@ -846,7 +839,7 @@ int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype,
   if (B > 65535 || H > 65535) return HDCM_EUNSUPPORTED;
   const int64_t tiles = (L + TC - 1) / TC;
   const int64_t unit = C > TC ? C / TC : 1;
-  int64_t st = env_int("HDCM_SLOT_SEG_TILES", 0);
+  int64_t st = hdcm_option_value(HDCM_OPT_SLOT_SEG_TILES);  // 0: automatic
   if (st == 0) {
     const int64_t bh = B * H > 0 ? B * H : 1;
     const int64_t want = (kTargetWorkgroups + bh - 1) / bh;

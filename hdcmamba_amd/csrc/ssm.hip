@@ -232,7 +232,6 @@ constexpr int kScanThreads = 512;
 constexpr int kScanCh = 32;  // channels per workgroup
 constexpr int kScanWaves = kScanThreads / kWave;
 constexpr int kHeaderBytes = 256;  // workspace header: epoch, finished-workgroup count
-constexpr int kDefaultSpinRounds = 256;
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 constexpr int kCachePolicySC1 = 16;       // buffer load cache policy: agent-scope coherent (sc1)
 
@@ -471,19 +470,25 @@ __device__ __forceinline__ void publish_total(unsigned long long* words, int64_t
 }
 
 // Compute and publish, with this call's tag, the totals of the tiles j0 + k for the set bits
-// k of `missing` (the rare path of the look-back).  All threads of the workgroup call it
-// together.
+// k of `missing` (the rare path of the look-back), and keep them in fill[k][channel] for the
+// caller's own fold.  All threads of the workgroup call it together.
 template <typename T>
 __device__ __forceinline__ void publish_missing(const T* __restrict__ projs, int64_t prs,
                                                 const float (&negA)[ScanShape<T>::E], unsigned long long* words, int64_t seq,
                                                 int64_t rowbase, int c0, int nch, int L, int ds, int ntiles, int j0,
-                                                unsigned long long missing, unsigned tag, ScanLds* lds) {
+                                                unsigned long long missing, unsigned tag, ScanLds* lds,
+                                                float (*fill)[kScanCh][2]) {
   while (missing != 0) {
-    const int jm = j0 + __builtin_ctzll(missing);
+    const int k = __builtin_ctzll(missing);
+    const int jm = j0 + k;
     missing &= missing - 1;
     float tA, tH;
     tile_total_streamed<T>(projs, prs, rowbase, jm, c0, nch, L, ds, negA, tA, tH, lds);
     publish_total(words, seq, ntiles, jm, nch, tA, tH, tag);
+    if (threadIdx.x < kScanCh) {
+      fill[k][threadIdx.x][0] = tA;
+      fill[k][threadIdx.x][1] = tH;
+    }
   }
 }
 
@@ -500,6 +505,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   __shared__ ScanLds s_lds;
   __shared__ float s_hin[kScanCh];
   __shared__ unsigned s_missing[kScanWaves][2];
+  __shared__ float s_fill[kWave][kScanCh][2];  // totals this workgroup computed for a window
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int cg = tid % CG, rg = tid / CG;
   const int tile = blockIdx.x, chb = blockIdx.y, b = blockIdx.z;
@@ -609,17 +615,29 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
       for (int k = 0; k < kScanWaves; ++k)
         all |= (unsigned long long)s_missing[k][0] | ((unsigned long long)s_missing[k][1] << 32);
       __syncthreads();
-      // (the round cap only guarantees termination: after one computing pass every total of
-      // the window has been stored by this workgroup and is read back in the next round)
-      if (all == 0 || round > spin_rounds + 2) break;
+      if (all == 0) break;
       if (round < spin_rounds) {
         __builtin_amdgcn_s_sleep(4);
         continue;
       }
-      // still missing after the polling budget: compute those tiles' totals here and publish
-      // them for their owners (the owner's own store later writes the same bits)
-      publish_missing<T>(projs, prs, negA, words, seq, rowbase, c0, nch, L, ds, ntiles, j0, all, tag, &s_lds);
+      // still missing after the polling budget: compute those tiles' totals here, publish
+      // them for their owners (the owner's own store later writes the same bits) and fold
+      // the values computed here for them; every other tile of the window was read with
+      // this call's tag by every wave.  No further read, so the loop ends here.
+      publish_missing<T>(projs, prs, negA, words, seq, rowbase, c0, nch, L, ds, ntiles, j0, all, tag, &s_lds,
+                         s_fill);
       __syncthreads();
+      if (act && ((all >> lane) & 1ull)) {
+#pragma unroll
+        for (int k = 0; k < CPW; ++k) {
+          const int c = w * CPW + k;
+          if (c < nch) {
+            va[k] = s_fill[lane][c][0];
+            vh[k] = s_fill[lane][c][1];
+          }
+        }
+      }
+      break;
     }
     // fold this window in tile order: inclusive lane scan, the total sits in lane 63
     scan_pairs<CPW>(va, vh);
@@ -684,12 +702,9 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   }
 }
 
-int spin_rounds_setting() {
-  const char* v = getenv("HDCM_SSM_SPIN_ROUNDS");  // test hook: 0 forces the compute-it-here path
-  if (!v || !*v) return kDefaultSpinRounds;
-  const int x = atoi(v);
-  return x >= 0 ? x : kDefaultSpinRounds;
-}
+// polling rounds before a missing total is computed here (HDCM_OPT_SSM_SPIN_ROUNDS; 0 forces
+// the compute-it-here path, a test hook)
+int spin_rounds_setting() { return hdcm_option_value(HDCM_OPT_SSM_SPIN_ROUNDS); }
 
 template <typename T>
 int launch(const void* projs, int64_t prs, const void* A_log, const float* h0, void* y,

@@ -6,9 +6,12 @@ construction consumes the global RNG (so ``torch.manual_seed(s)`` followed by
 construction yields the same weights) are those of the reference.  The forward of a
 block runs, per layer:
 
-    norm_conv (HIP)  ->  in_proj (hipBLASLt GEMM)  ->  ssm (HIP) and slot+gate (HIP)
-    writing one `combined` row buffer  ->  row LayerNorm (HIP, in place)
-    ->  out_proj GEMM with the residual fused (addmm)
+    norm_conv (HIP)  ->  in_proj (hipBLASLt GEMM)  ->  ssm (HIP) and slot state, scan and
+    gate (HIP) writing one `combined` row buffer
+    ->  bf16 without autograd: one HIP GEMM applying the row LayerNorm of `combined` in its
+        epilogue (row statistics handed over by the ssm and gate kernels), out_proj and the
+        residual add, in place on the residual stream;
+        otherwise: row LayerNorm (HIP, in place) -> out_proj with the residual (addmm)
 
 Intended semantics are computed (see the oracle's docstring for the reference kernel
 defects that are not reproduced).  Only GPU tensors are accepted; there is no CPU path.

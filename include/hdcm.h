@@ -44,7 +44,9 @@ typedef enum {
   HDCM_ETOOBIG = -6       /* input larger than a no-allocation entry point's fixed scratch */
 } hdcm_status;
 
-#define HDCM_ABI_VERSION 1
+/* 2: hdcm_ssm_fwd and hdcm_slot_gate_fwd take row_stats and its part stride; the scan's
+ *    workspace contract (zero before its first use, then kept between calls); launch options. */
+#define HDCM_ABI_VERSION 2
 
 int hdcm_abi_version(void);
 const char* hdcm_strerror(int status);
@@ -62,6 +64,23 @@ const char* hdcm_strerror(int status);
  */
 int hdcm_time_launches(void* const* start_events, void* const* stop_events, int n);
 int hdcm_timed_launch_count(void);
+
+/*
+ * Launch options, for tests and tuning.  Their values when the library loads come from the
+ * environment variables named below, read once; hdcm_set_option changes one for every later
+ * launch of the process (a recorded graph keeps the values current at its capture).
+ *  HDCM_OPT_SSM_SPIN_ROUNDS (env HDCM_SSM_SPIN_ROUNDS, default 256): polling rounds of the
+ *    scan's look-back before a workgroup computes a missing earlier tile total itself
+ *    (0 forces that path).  Results do not depend on it.
+ *  HDCM_OPT_SLOT_SEG_TILES (env HDCM_SLOT_SEG_TILES, default 0 = automatic): row tiles per
+ *    segment of the slot kernels.  Results do not depend on it beyond fp32 rounding.
+ * hdcm_set_option returns HDCM_EINVAL for an unknown option or a value out of range
+ * (both take 0 .. 2^20); hdcm_get_option returns the current value (0 for an unknown one).
+ * No counterpart in the reference (its launch table, model.py:12-19, is fixed).
+ */
+typedef enum { HDCM_OPT_SSM_SPIN_ROUNDS = 1, HDCM_OPT_SLOT_SEG_TILES = 2 } hdcm_option;
+int hdcm_set_option(int option, int value);
+int hdcm_get_option(int option);
 
 /*
  * LayerNorm over D (biased variance, eps) followed by the causal depthwise

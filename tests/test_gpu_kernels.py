@@ -20,7 +20,7 @@ def _say(*a):
 
 # ----------------------------------------------------------------------------- norm_conv
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("D,L", [(256, 1), (256, 5), (768, 100), (1024, 257), (2048, 64)])
+@pytest.mark.parametrize("D,L", [(256, 1), (256, 5), (768, 100), (1024, 257), (2048, 64), (3072, 37)])
 def test_norm_conv(dev, dtype, D, L):
     _say("norm_conv", dtype, D, L)
     g = torch.Generator().manual_seed(D + L)
@@ -33,6 +33,14 @@ def test_norm_conv(dev, dtype, D, L):
     out = _ops.norm_conv(x.to(dev), ln_w.to(dev), ln_b.to(dev), cw.to(dev), cb.to(dev), 1e-5)
     ref = oracle.norm_conv(x, ln_w, ln_b, cw, cb, 1e-5)
     assert_close(out, ref, dtype, "norm_conv")
+
+
+@pytest.mark.parametrize("D,L", [(2560, 50), (4096, 37), (6144, 19)])
+def test_norm_conv_wide_rows_bf16(dev, D, L):
+    """bf16 rows wider than 32 columns per lane take the one-row-at-a-time path (up to the 6144
+    limit); L not a multiple of the 16-row run covers its partial last run."""
+    _say("norm_conv wide", D, L)
+    test_norm_conv(dev, torch.bfloat16, D, L)
 
 
 def test_norm_conv_batch_strided(dev):
@@ -117,7 +125,7 @@ def test_ssm(dev, dtype, ds, B, L):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_ssm_totals_computed_for_their_owners(dev, dtype, monkeypatch):
+def test_ssm_totals_computed_for_their_owners(dev, dtype):
     """With no polling budget a workgroup that finds an earlier tile's total missing computes
     it itself and publishes it for its owner; the outputs are bit-identical to the default
     (the same code computes every total), with a start state and the final state.  L=40000:
@@ -128,12 +136,14 @@ def test_ssm_totals_computed_for_their_owners(dev, dtype, monkeypatch):
     pd, ad = projs.to(dev), A_log.to(dev)
     h0 = torch.randn(B, ds, generator=torch.Generator().manual_seed(3)).to(dev)
     outs = []
-    for spin in (None, "0"):
-        if spin is not None:
-            monkeypatch.setenv("HDCM_SSM_SPIN_ROUNDS", spin)
+    for spin in (None, 0):
         y = torch.empty(B, L, ds, device=dev, dtype=dtype)
         hf = torch.empty(B, ds, device=dev)
-        _ops.ssm(pd, ad, ds, y, h0=h0, h_final=hf)
+        if spin is None:
+            _ops.ssm(pd, ad, ds, y, h0=h0, h_final=hf)
+        else:
+            with _ops.option("ssm_spin_rounds", spin):
+                _ops.ssm(pd, ad, ds, y, h0=h0, h_final=hf)
         torch.cuda.synchronize()
         outs.append((y, hf))
     assert torch.equal(outs[0][0], outs[1][0])
@@ -294,14 +304,14 @@ def test_slot_attend(dev, dtype, B, L, dm, H, C, phi, reverse):
     assert err <= lim, ("chain", err)
 
 
-def test_slot_segments_env(dev, monkeypatch):
+def test_slot_segments_option(dev):
     """Different segment lengths (state pre-pass on/off) give the same result."""
     dm, ds, H, C, B, L = 256, 64, 4, 64, 1, 1024
     projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, torch.float32, seed=3)
     outs = []
-    for st in ("1", "2", "16"):
-        monkeypatch.setenv("HDCM_SLOT_SEG_TILES", st)
-        outs.append(_run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C)[0])
+    for st in (1, 2, 16):
+        with _ops.option("slot_seg_tiles", st):
+            outs.append(_run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C)[0])
     for o in outs[1:]:
         assert_close(o, outs[0], torch.float32, "segment invariance")
 
