@@ -340,7 +340,7 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
   HDCM_CHECK_ARG(y_col >= 0 && g_col >= 0 && out_row_stride >= y_col + ds && out_row_stride >= g_col + dm,
                  HDCM_EINVAL);
   const int64_t hd = dm / H;
-  HDCM_CHECK_ARG((hd == 32 || hd == 64 || hd == 96 || hd == 128) && H < 65535 && B <= 65535 &&
+  HDCM_CHECK_ARG(hd >= 16 && hd <= 128 && hd % 16 == 0 && H < 65535 && B <= 65535 &&
                      proj_row_stride < ((int64_t)1 << 31),
                  HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(C < ((int64_t)1 << 24), HDCM_EUNSUPPORTED);
@@ -357,14 +357,22 @@ extern "C" int hdcm_mixer_step_fwd(const void* projs, int64_t proj_row_stride, i
     return hdcm_launch_status();                                                                             \
   }
   if (dtype == HDCM_F32) {
+    HDCM_MIX_CASE(float, 16)
     HDCM_MIX_CASE(float, 32)
+    HDCM_MIX_CASE(float, 48)
     HDCM_MIX_CASE(float, 64)
+    HDCM_MIX_CASE(float, 80)
     HDCM_MIX_CASE(float, 96)
+    HDCM_MIX_CASE(float, 112)
     HDCM_MIX_CASE(float, 128)
   } else {
+    HDCM_MIX_CASE(bf16_t, 16)
     HDCM_MIX_CASE(bf16_t, 32)
+    HDCM_MIX_CASE(bf16_t, 48)
     HDCM_MIX_CASE(bf16_t, 64)
+    HDCM_MIX_CASE(bf16_t, 80)
     HDCM_MIX_CASE(bf16_t, 96)
+    HDCM_MIX_CASE(bf16_t, 112)
     HDCM_MIX_CASE(bf16_t, 128)
   }
 #undef HDCM_MIX_CASE

@@ -13,7 +13,10 @@
 //   dw_k   = sum_t go[t] u[t-3+k]
 //
 // norm_conv_bwd_rows_kernel: one wave per 16-row run, lanes own 16-byte column groups (as
-// the forward); a ring holds go[t..t+3]; writes dx and the row statistics (mu_t, r_t).
+// the forward); a ring holds go[t..t+3]; writes dx and the row statistics (mu_t, r_t).  Rows
+// wider than 8 groups per lane (fp32) or 4 (bf16), i.e. D > 2048, take the same kernel with
+// the four waves of a workgroup sharing each row (WPR = 4: 256 column lanes, row sums
+// finished across the waves in LDS), up to the forward's 768 groups per row.
 // norm_conv_bwd_cols_kernel: thread = one 16-byte column group x one chunk of rows; walks
 // the chunk keeping go[t..t+3] and u[t-3..t] in registers, with the next four rows' loads in
 // flight while the current four are summed, and writes the seven column sums of its chunk.  colsum_kernel sums the chunks in a fixed order (the result does not depend
@@ -30,12 +33,12 @@ constexpr int kChunk = 64;    // rows per chunk, column kernel
 constexpr int kStep = 4;      // rows loaded ahead, column kernel
 constexpr int kColThreads = 64;
 
-template <typename T, int NG>
+template <typename T, int NG, int CW = kWave>
 __device__ __forceinline__ void ld_row(float (&v)[NG][Vec<T>::N], const T* row, int lane, int G, bool valid) {
   constexpr int E = Vec<T>::N;
 #pragma unroll
   for (int i = 0; i < NG; ++i) {
-    const int g = lane + kWave * i;
+    const int g = lane + CW * i;
     if (valid && g < G) {
       load16<T>(row + (int64_t)g * E, v[i]);
     } else {
@@ -45,16 +48,48 @@ __device__ __forceinline__ void ld_row(float (&v)[NG][Vec<T>::N], const T* row, 
   }
 }
 
-template <typename T, int NG>
+// WPR waves per row: 1 (each wave its own run of rows) or kRowsWPB (the workgroup's waves
+// share one run, thread = column lane).
+template <typename T, int NG, int WPR>
 __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
     const T* __restrict__ go, int64_t g_bs, int64_t g_rs, const T* __restrict__ x, int64_t x_bs, int64_t x_rs,
     const T* __restrict__ ln_w, const T* __restrict__ conv_w, T* __restrict__ dx, int64_t d_bs, int64_t d_rs,
     float2* __restrict__ stats, int L, int D, float eps) {
+  static_assert(WPR == 1 || WPR == kRowsWPB, "a row is one wave or the whole workgroup");
   constexpr int E = Vec<T>::N;
-  const int lane = threadIdx.x & (kWave - 1);
+  constexpr int CW = WPR * kWave;  // column lanes of a row
+  __shared__ float red[2][kRowsWPB][2];
   const int wave = threadIdx.x / kWave;
-  const int64_t t0 = ((int64_t)blockIdx.x * kRowsWPB + wave) * kRunRows;
-  if (t0 >= L) return;
+  const int lane = WPR == 1 ? (int)(threadIdx.x & (kWave - 1)) : (int)threadIdx.x;  // column lane
+  const int64_t t0 = (WPR == 1 ? (int64_t)blockIdx.x * kRowsWPB + wave : (int64_t)blockIdx.x) * kRunRows;
+  if (t0 >= L) return;  // (WPR > 1: the same for every wave of the workgroup)
+  // Row totals of one or two values: within the wave, then (WPR > 1) across the waves through
+  // LDS.  Two buffers used in turn: a buffer is written again only two reductions later, after
+  // the barrier of the reduction between, which every thread passes after reading it.
+  int parity = 0;
+  auto row_total2 = [&](float& a, float& c) {
+    a = wave_total(a);
+    c = wave_total(c);
+    if constexpr (WPR > 1) {
+      if ((threadIdx.x & (kWave - 1)) == 0) {
+        red[parity][wave][0] = a;
+        red[parity][wave][1] = c;
+      }
+      __syncthreads();
+      a = c = 0.f;
+#pragma unroll
+      for (int k = 0; k < WPR; ++k) {
+        a += red[parity][k][0];
+        c += red[parity][k][1];
+      }
+      parity ^= 1;
+    }
+  };
+  auto row_total = [&](float a) {
+    float c = 0.f;
+    row_total2(a, c);
+    return a;
+  };
   const int b = blockIdx.y;
   const int G = D / E;
   const float invD = 1.0f / (float)D;
@@ -65,7 +100,7 @@ __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
   float gw[NG][E], cw[4][NG][E];
 #pragma unroll
   for (int i = 0; i < NG; ++i) {
-    const int g = lane + kWave * i;
+    const int g = lane + CW * i;
     float c4[4 * E];
     if (g < G) {
       load16<T>(ln_w + g * E, gw[i]);
@@ -85,28 +120,28 @@ __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
 
   // go ring: r0 = go[t], r1 = go[t+1], r2 = go[t+2]; go[t+3] is loaded each row
   float r0[NG][E], r1[NG][E], r2[NG][E];
-  ld_row<T, NG>(r0, gb + t0 * g_rs, lane, G, true);
-  ld_row<T, NG>(r1, gb + (t0 + 1) * g_rs, lane, G, t0 + 1 < L);
-  ld_row<T, NG>(r2, gb + (t0 + 2) * g_rs, lane, G, t0 + 2 < L);
+  ld_row<T, NG, CW>(r0, gb + t0 * g_rs, lane, G, true);
+  ld_row<T, NG, CW>(r1, gb + (t0 + 1) * g_rs, lane, G, t0 + 1 < L);
+  ld_row<T, NG, CW>(r2, gb + (t0 + 2) * g_rs, lane, G, t0 + 2 < L);
 
 #pragma unroll 1
   for (int r = 0; r < kRunRows; ++r) {
     const int64_t t = t0 + r;
     if (t >= L) break;
     float r3[NG][E], xv[NG][E];
-    ld_row<T, NG>(r3, gb + (t + 3) * g_rs, lane, G, t + 3 < L);
-    ld_row<T, NG>(xv, xb + t * x_rs, lane, G, true);
+    ld_row<T, NG, CW>(r3, gb + (t + 3) * g_rs, lane, G, t + 3 < L);
+    ld_row<T, NG, CW>(xv, xb + t * x_rs, lane, G, true);
     // row statistics of x[t]
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NG; ++i)
 #pragma unroll
       for (int e = 0; e < E; ++e) s += xv[i][e];
-    const float mean = wave_total(s) * invD;
+    const float mean = row_total(s) * invD;
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
-      const bool ok = (lane + kWave * i) < G;
+      const bool ok = (lane + CW * i) < G;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
         const float c = ok ? xv[i][e] - mean : 0.f;
@@ -114,7 +149,7 @@ __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
         q += c * c;
       }
     }
-    const float rstd = rsqrtf(wave_total(q) * invD + eps);
+    const float rstd = rsqrtf(row_total(q) * invD + eps);
     // gh = (sum_k w_k go[t+3-k]) * g, and the two row sums of the LayerNorm backward
     float gh[NG][E];
     float s1 = 0.f, s2 = 0.f;
@@ -129,10 +164,11 @@ __global__ __launch_bounds__(kRowsWPB* kWave) void norm_conv_bwd_rows_kernel(
         s1 += gh[i][e];
         s2 += gh[i][e] * xv[i][e];
       }
-    const float m1 = wave_total(s1) * invD, m2 = wave_total(s2) * invD;
+    row_total2(s1, s2);
+    const float m1 = s1 * invD, m2 = s2 * invD;
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
-      const int g = lane + kWave * i;
+      const int g = lane + CW * i;
       float o[E];
 #pragma unroll
       for (int e = 0; e < E; ++e) o[e] = rstd * (gh[i][e] - m1 - xv[i][e] * m2);
@@ -319,18 +355,33 @@ int launch_bwd(const void* go, int64_t g_bs, int64_t g_rs, const void* x, int64_
   float* part = (float*)((char*)ws + ((B * L * sizeof(float2) + 255) / 256) * 256);
   const int64_t nchunk = chunks_of(L);
   const dim3 rgrid((unsigned)((L + kRowsWPB * kRunRows - 1) / (kRowsWPB * kRunRows)), (unsigned)B);
+  const dim3 rgrid_wide((unsigned)((L + kRunRows - 1) / kRunRows), (unsigned)B);  // a run per workgroup
 #define HDCM_BWD_ROWS(N)                                                                                         \
   if (ng <= N)                                                                                                   \
-    HDCM_LAUNCH((norm_conv_bwd_rows_kernel<T, N>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
+    HDCM_LAUNCH((norm_conv_bwd_rows_kernel<T, N, 1>), rgrid, dim3(kRowsWPB * kWave), 0, s, (const T*)go,   \
                        g_bs, g_rs, (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)conv_w, (T*)dx, d_bs, d_rs, \
                        stats, (int)L, (int)D, eps);
   // up to 4 groups per lane: one instance per count; fp32 rows of 1028 to 2048 columns (5 to
   // 8 groups) share an 8-group instance whose lanes past the row idle (256 VGPRs + 108 AGPRs,
-  // no spills; bf16 rows up to 2048 columns fit in 4 groups)
+  // no spills; bf16 rows up to 2048 columns fit in 4 groups); wider rows (up to 768 groups:
+  // bf16 6144, fp32 3072 columns) spread over the 256 threads of a workgroup, 3 groups each
+  constexpr int kWideGroups = 3;
+  bool launched = true;
   HDCM_BWD_ROWS(1)
-  else HDCM_BWD_ROWS(2) else HDCM_BWD_ROWS(3) else HDCM_BWD_ROWS(4) else if constexpr (sizeof(T) == 4) {
-    HDCM_BWD_ROWS(8) else return HDCM_EUNSUPPORTED;
-  } else return HDCM_EUNSUPPORTED;
+  else HDCM_BWD_ROWS(2) else HDCM_BWD_ROWS(3) else HDCM_BWD_ROWS(4) else launched = false;
+  if constexpr (sizeof(T) == 4) {
+    if (!launched && ng <= 8) {
+      HDCM_BWD_ROWS(8)
+      launched = true;
+    }
+  }
+  if (!launched && G <= kWideGroups * kRowsWPB * kWave) {
+    HDCM_LAUNCH((norm_conv_bwd_rows_kernel<T, kWideGroups, kRowsWPB>), rgrid_wide, dim3(kRowsWPB * kWave), 0, s,
+                (const T*)go, g_bs, g_rs, (const T*)x, x_bs, x_rs, (const T*)ln_w, (const T*)conv_w, (T*)dx, d_bs,
+                d_rs, stats, (int)L, (int)D, eps);
+    launched = true;
+  }
+  if (!launched) return HDCM_EUNSUPPORTED;
 #undef HDCM_BWD_ROWS
   int st = hdcm_launch_status();
   if (st) return st;
@@ -363,7 +414,7 @@ extern "C" int hdcm_norm_conv_bwd(const void* grad_out, int64_t g_batch_stride, 
   HDCM_CHECK_ARG(B >= 0 && L >= 0 && D > 0, HDCM_EINVAL);
   const int E = 16 / hdcm_elt_size(dtype);
   HDCM_CHECK_ARG(D % E == 0, HDCM_EALIGN);
-  HDCM_CHECK_ARG(D <= 2048, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(D / (16 / hdcm_elt_size(dtype)) <= 768, HDCM_EUNSUPPORTED);  // bf16 6144, fp32 3072 (the forward's)
   HDCM_CHECK_ARG(B <= 65535 && L < (int64_t)1 << 30 && (L + kChunk - 1) / kChunk <= 65535, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(hdcm_aligned16(ln_w) && hdcm_aligned16(ln_b) && hdcm_aligned16(conv_w), HDCM_EALIGN);
   if (B == 0 || L == 0)  // no rows (strides unused): the parameter gradients are zero

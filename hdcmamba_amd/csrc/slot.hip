@@ -17,9 +17,17 @@
 // and for t in the tile  y_t = intra_t + gamma^(t-p) phi(q_t) . S_eff,
 //   S_eff = gamma*W + gamma^(p-cs)*A.
 // When C divides TC every tile start is a chunk boundary (W = 0) and the cross-chunk
-// factor gamma^-1 appears inside the tile's score matrix instead.
+// factor gamma^-1 appears inside the tile's score matrix instead.  Any other C is walked in
+// chunk-confined tiles: each chunk is covered by ceil(C/TC) tiles of up to TC rows (the last
+// one shorter), so no tile straddles a chunk boundary (the rows past a short tile are zero
+// in LDS) and the W/A split above applies unchanged.
 //
-// Parallelism: the sequence is cut into segments of seg_tiles tiles that start on chunk
+// Head dims: any multiple of 16 up to 128.  The contractions over the head dim run in K=32
+// steps, so for hd not a multiple of 32 the phi(q), phi(k) and S_eff^T tiles carry zero
+// columns up to the next multiple of 32 (written once per workgroup); contractions over
+// tokens and the value columns use the hd/16 16-wide tiles as they are.
+//
+// Parallelism: the sequence is cut into segments of whole tiles that start on chunk
 // boundaries.  slot_state_kernel computes each segment's contribution U_s to A (from k
 // and v only), slot_scan_kernel turns them into the state at every segment start, and
 // slot_gate_kernel walks each (batch, head, segment) with its own start state.  That
@@ -71,7 +79,8 @@ template <typename T, int HD, int TC>
 struct Lds {
   static constexpr bool TR = sizeof(T) == 2;
   static constexpr int E = 16 / sizeof(T);
-  static constexpr int PQ = HD + E;
+  static constexpr int HDK = (HD + 31) / 32 * 32;  // contraction width over the head dim
+  static constexpr int PQ = HDK + E;
   static constexpr int PV = TR ? HD + 16 : TC + E;
   static constexpr int tileQ = TC * PQ;
   static constexpr int tileV = TR ? TC * PV : HD * PV;
@@ -79,7 +88,7 @@ struct Lds {
   static constexpr int oK = oQ + tileQ;    // phi(k)
   static constexpr int oKd = oK + tileQ;   // k~ = phi(k) * gamma^(tlen-1-i)
   static constexpr int oV = oKd + tileV;   // v
-  static constexpr int oS = oV + tileV;    // S_eff^T [HD][HD]
+  static constexpr int oS = oV + tileV;    // S_eff^T [HD][HDK]
   static constexpr int total = oS + HD * PQ;
   // the state pre-pass uses only k~ and v
   static constexpr int stKd = 0;
@@ -180,19 +189,23 @@ __device__ __forceinline__ Frag<float> frag_scale(const Frag<float>& f, float c)
 }
 
 // Tile loader.  The tile's q, k, v (blocks 0,1,2) or only k, v (B0=1, NB=2) are split
-// into 16-byte groups; group idx = tid + 256*it covers block B0 + (256*it)/(TC*GPR), row i,
-// column group cg.  Block B0+k starts boff[k] columns after the tile base (the q, k, v
-// column blocks of one row buffer).  TC*GPR is a multiple of 256, so the block of each
-// iteration is uniform and rows advance by whole tiles between calls.  The row stride may
-// be negative (a sequence walked backwards from its last row).
+// into 16-byte groups, GPT = TC*GPR of them per block; iteration it covers block
+// B0 + it/IPB, group idx = tid + 256*(it%IPB) (row idx/GPR, column group idx%GPR), so the
+// block of each iteration is uniform and rows advance by whole tiles between calls.  When
+// GPT is not a multiple of 256 the threads past it in a block's last iteration are idle:
+// they load row 0, column group 0 of the block (in bounds) and stage nothing.  Block B0+k
+// starts boff[k] columns after the tile base (the q, k, v column blocks of one row buffer).
+// The row stride may be negative (a sequence walked backwards from its last row).
 template <typename T, int HD, int TC, int B0, int NB>
 struct TileLoader {
   static constexpr int E = Vec<T>::N;
   static constexpr int GPR = HD / E;
-  static constexpr int NL = NB * TC * GPR / kThreads;
-  static constexpr int IPB = TC * GPR / kThreads;        // iterations per block
-  static constexpr bool SCALAR = (kThreads % GPR) == 0;  // row step per iteration is uniform
-  static_assert((TC * GPR) % kThreads == 0, "tile block must be a multiple of the workgroup");
+  static constexpr int GPT = TC * GPR;                           // groups per block
+  static constexpr int IPB = (GPT + kThreads - 1) / kThreads;    // iterations per block
+  static constexpr int NL = NB * IPB;
+  static constexpr bool EXACT = GPT % kThreads == 0;
+  static constexpr bool SCALAR = EXACT && (kThreads % GPR) == 0;  // row step per iteration is uniform
+  static_assert(HD % E == 0, "head dim in 16-byte groups");
   // With SCALAR, iteration it reads row tid/GPR + (it % IPB) * (kThreads/GPR) of block
   // B0 + it/IPB at column group tid%GPR: one per-thread offset plus uniform strides.
   int64_t base;
@@ -201,6 +214,9 @@ struct TileLoader {
   int boff[NB];
   int64_t off[SCALAR ? 1 : NL];
   int row[SCALAR ? 1 : NL];
+  __device__ __forceinline__ static bool valid(int it, int tid) {
+    return EXACT || tid + kThreads * (it % IPB) < GPT;
+  }
   __device__ __forceinline__ TileLoader(int64_t prs_, const int (&boffs)[NB], int tid) : prs(prs_) {
 #pragma unroll
     for (int k = 0; k < NB; ++k) boff[k] = boffs[k];
@@ -209,11 +225,15 @@ struct TileLoader {
     if constexpr (!SCALAR) {
 #pragma unroll
       for (int it = 0; it < NL; ++it) {
-        const int idx = tid + kThreads * it;
-        const int blk = B0 + (kThreads * it) / (TC * GPR);
-        const int rem = idx % (TC * GPR);
-        row[it] = rem / GPR;
-        off[it] = (int64_t)row[it] * prs + boff[blk - B0] + (rem % GPR) * E;
+        const int idx = tid + kThreads * (it % IPB);
+        const int blk = it / IPB;
+        if (valid(it, tid)) {
+          row[it] = idx / GPR;
+          off[it] = (int64_t)row[it] * prs + boff[blk] + (idx % GPR) * E;
+        } else {
+          row[it] = 0;
+          off[it] = boff[blk];
+        }
       }
     }
   }
@@ -252,10 +272,10 @@ __device__ __forceinline__ void stage_tile_impl(const uint4 (&raw)[TileLoader<T,
   T* sV = sm + (STATE_ONLY ? LD::stV : LD::oV);
 #pragma unroll
   for (int it = 0; it < TL::NL; ++it) {
-    const int idx = tid + kThreads * it;
-    const int blk = B0 + (kThreads * it) / (TC * GPR);
-    const int rem = idx % (TC * GPR);
-    const int i = rem / GPR, cg = rem % GPR;
+    if (!TL::valid(it, tid)) continue;
+    const int idx = tid + kThreads * (it % TL::IPB);
+    const int blk = B0 + it / TL::IPB;
+    const int i = idx / GPR, cg = idx % GPR;
     const bool ok = FULL || i < tlen;
     if (blk == 0) {  // phi(q), row-major
       float f[E];
@@ -306,6 +326,23 @@ __device__ __forceinline__ void stage_tile(const uint4 (&raw)[TileLoader<T, HD, 
     stage_tile_impl<T, HD, TC, B0, NB, STATE_ONLY, PHI, false>(raw, sm, tlen, lg2, tid);
 }
 
+// Zero the contraction padding of the row-major tiles (columns HD .. HDK-1 of phi(q), phi(k)
+// and S_eff^T), which staging never writes: once per workgroup, before the first barrier.
+template <typename T, int HD, int TC>
+__device__ __forceinline__ void zero_contraction_pad(T* sm, int tid) {
+  using LD = Lds<T, HD, TC>;
+  constexpr int PAD = LD::HDK - HD;
+  if constexpr (PAD > 0) {
+    constexpr int ROWS = 2 * TC + HD;  // phi(q) and phi(k) rows, then S_eff^T rows
+    for (int k = tid; k < ROWS * PAD; k += kThreads) {
+      const int r = k / PAD, c = HD + k % PAD;
+      T* t = r < TC ? sm + LD::oQ + r * LD::PQ : r < 2 * TC ? sm + LD::oK + (r - TC) * LD::PQ
+                                                           : sm + LD::oS + (r - 2 * TC) * LD::PQ;
+      t[c] = T();
+    }
+  }
+}
+
 // PHI: feature map phi on q and k (else the identity).  EPI: GroupNorm + sigmoid gate
 // epilogue (else y itself is stored).  CHAIN (without EPI): each stored value is multiplied by
 // phi'(z) = 1 (z > 0) else exp(z), z read from zb at the output's own row and column (zb has
@@ -315,7 +352,7 @@ template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI
 __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int k_off, int v_off, int g_off, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
-    float gn_eps, const float* __restrict__ Ain, int seg_tiles, int nseg, T* __restrict__ out,
+    float gn_eps, const float* __restrict__ Ain, int seg_rows, int nseg, T* __restrict__ out,
     int64_t ors, int out_col, float* __restrict__ S_final, float* __restrict__ row_stats, int64_t stats_ps,
     const T* __restrict__ zb = nullptr, int64_t zrs = 0) {
   using LD = Lds<T, HD, TC>;
@@ -324,9 +361,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   __shared__ __attribute__((aligned(16))) T sm[LD::total];
   __shared__ float sgw[HD], sgb[HD];
   constexpr int NVT = HD / 16;  // 16-wide tiles across the head dim
-  constexpr int NKS = HD / 32;  // K=32 steps across the head dim
-  constexpr int NJS = TC / 32;  // K=32 steps across the tile rows
-  constexpr int NIT = TC / 16;  // 16-row query tiles
+  constexpr int NKS = LD::HDK / 32;  // K=32 steps across the head dim (zero-padded)
+  constexpr int NJS = TC / 32;       // K=32 steps across the tile rows
+  constexpr int NIT = TC / 16;       // 16-row query tiles
   constexpr int OWN = (NVT + kWaves - 1) / kWaves;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
@@ -340,10 +377,14 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     gnw_raw = gn_w[h * HD + tid % HD];
     gnb_raw = gn_b[h * HD + tid % HD];
   }
-  const bool one_chunk = cshift >= 31;  // C >= TC: every pair in a tile shares a chunk
+  // cshift >= 31: tiles are chunk-confined (C does not divide TC), so every pair in a tile
+  // shares a chunk; otherwise tiles hold TC/C whole chunks
+  const bool one_chunk = cshift >= 31;
   const int64_t rowbase = (int64_t)b * L;
-  const int p_begin = seg * seg_tiles * TC;
-  const int p_end = min(L, p_begin + seg_tiles * TC);
+  const int p_begin = seg * seg_rows;
+  const int p_end = min(L, p_begin + seg_rows);
+  // rows of the tile starting at p (p_end and chunk ends are tile ends)
+  auto tile_len = [&](int p) { return one_chunk ? min(min(TC, p_end - p), C - p % C) : min(TC, p_end - p); };
   const T* colbase = projs + q_col + h * HD;
   // the gate (EPI), or the chain rule's z (CHAIN: same positions as the output)
   const T* gatebase = CHAIN ? zb + out_col + h * HD : colbase + g_off;
@@ -368,7 +409,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
 
   const TL loader(prs, {0, k_off, v_off}, tid);
   uint4 raw[TL::NL];
-  loader.load(raw, colbase + (rowbase + p_begin) * prs, min(TC, L - p_begin));
+  loader.load(raw, colbase + (rowbase + p_begin) * prs, tile_len(p_begin));
 
   // Gate values of this lane's output positions (row 16*w + l16 of a tile), kept as
   // stored.  They are loaded one tile ahead, right after the current tile's outputs, so
@@ -379,15 +420,14 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   //   bf16 with 16-byte aligned output rows (PAIRS): 16-byte runs in the exchanged layout
   //   of the output stage below: for each pair of tiles, columns
   //   32*pp + 16*(kg&1) + 8*(kg>>1) .. +7.  Otherwise as fp32 (8 bytes each).
-  constexpr bool kPairs = PAIRS && sizeof(T) == 2;
+  constexpr bool kPairs = PAIRS && sizeof(T) == 2 && NVT % 2 == 0;  // odd tile counts: 8-byte runs
   constexpr int NG = kPairs ? NVT / 2 : NVT;
-  static_assert(!kPairs || NVT % 2 == 0, "tile pairs");
   const int gcol = kPairs ? 16 * (kg & 1) + 8 * (kg >> 1) : 4 * kg;
   const int gstep = kPairs ? 32 : 16;
   uint4 graw[NG];
   const int giq = (w < NIT ? w : 0) * 16 + l16;
   auto load_gate = [&](int pt) {
-    const int tl = min(TC, L - pt);
+    const int tl = tile_len(pt);
     const T* grow = gatebase + (rowbase + pt + (giq < tl ? giq : 0)) * grs + gcol;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -409,9 +449,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     sgw[tid] = to_f<T>(gnw_raw);
     sgb[tid] = to_f<T>(gnb_raw);
   }
+  zero_contraction_pad<T, HD, TC>(sm, tid);  // ordered before every read by the loop's barriers
 
-  for (int p = p_begin; p < p_end; p += TC) {
-    const int tlen = min(TC, L - p);
+  for (int p = p_begin, tlen = tile_len(p_begin); p < p_end; p += tlen, tlen = p < p_end ? tile_len(p) : 0) {
     __syncthreads();
     stage_tile<T, HD, TC, 0, 3, false, PHI>(raw, sm, tlen, lg2, tid);
     // S_eff^T for this tile: gamma*W + gamma^(p-cs)*A (A alone when C divides TC).
@@ -439,8 +479,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     }
     {
       // next tile, or this tile again (already in cache) after the last: a fixed load count
-      const int pn = p + TC < p_end ? p + TC : p;
-      loader.load(raw, colbase + (rowbase + pn) * prs, min(TC, L - pn));
+      const int pn = p + tlen < p_end ? p + tlen : p;
+      loader.load(raw, colbase + (rowbase + pn) * prs, tile_len(pn));
     }
     __syncthreads();
 
@@ -627,7 +667,7 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
         }
       }
       // next tile's gate (this tile's again after the last: a fixed load count)
-      if constexpr (EPI || CHAIN) load_gate(p + TC < p_end ? p + TC : p);
+      if constexpr (EPI || CHAIN) load_gate(p + tlen < p_end ? p + tlen : p);
     }
 
     // ---- state update: (W or A) <- gamma^tlen * (W or A) + K~^T V
@@ -692,7 +732,7 @@ template <typename T, int HD, int TC, bool PHI>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(const T* __restrict__ projs,
                                                               int64_t prs, int k_col, int v_off,
                                                               int L, const T* __restrict__ gamma,
-                                                              int seg_tiles, int nseg,
+                                                              int seg_rows, int nseg,
                                                               float* __restrict__ U) {
   using LD = Lds<T, HD, TC>;
   using TL = TileLoader<T, HD, TC, 1, 2>;
@@ -706,8 +746,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
   const int h = blockIdx.x, seg = blockIdx.y, b = blockIdx.z, H = gridDim.x;
   const float lg2 = log2f(to_f<T>(gamma[h]));
   const int64_t rowbase = (int64_t)b * L;
-  const int p_begin = seg * seg_tiles * TC;
-  const int p_end = min(L, p_begin + seg_tiles * TC);
+  const int p_begin = seg * seg_rows;
+  const int p_end = min(L, p_begin + seg_rows);
   const T* colbase = projs + k_col + h * HD;
 
   f32x4_t st[OWN][NVT];
@@ -724,15 +764,16 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
   const TL loader(prs, {0, v_off}, tid);
   uint4 raw0[TL::NL], raw1[TL::NL];
   const T* tbase = colbase + rowbase * prs;
+  // U_s is a decayed sum over the segment's rows, so the tiles need not follow chunks
   const int p1 = p_begin + TC < p_end ? p_begin + TC : p_begin;
-  loader.load(raw0, tbase + (int64_t)p_begin * prs, min(TC, L - p_begin));
-  loader.load(raw1, tbase + (int64_t)p1 * prs, min(TC, L - p1));
+  loader.load(raw0, tbase + (int64_t)p_begin * prs, min(TC, p_end - p_begin));
+  loader.load(raw1, tbase + (int64_t)p1 * prs, min(TC, p_end - p1));
 
   auto step = [&](uint4 (&raw)[TL::NL], int p, int tlen) {
     __syncthreads();
     stage_tile<T, HD, TC, 1, 2, true, PHI>(raw, sm, tlen, lg2, tid);
     const int pn = p + 2 * TC < p_end ? p + 2 * TC : p;
-    loader.load(raw, tbase + (int64_t)pn * prs, min(TC, L - pn));
+    loader.load(raw, tbase + (int64_t)pn * prs, min(TC, p_end - pn));
     __syncthreads();
     const float gt = fexp2((float)tlen * lg2);
 #pragma unroll
@@ -757,9 +798,9 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 2 : 4) void slot_state_kernel(c
     }
   };
   for (int p = p_begin; p < p_end; p += 2 * TC) {
-    step(raw0, p, min(TC, L - p));
+    step(raw0, p, min(TC, p_end - p));
     const bool second = p + TC < p_end;
-    step(raw1, second ? p + TC : p, second ? min(TC, L - p - TC) : 0);
+    step(raw1, second ? p + TC : p, second ? min(TC, p_end - p - TC) : 0);
   }
   float* u = U + (((int64_t)b * H + h) * nseg + seg) * HD * HD;
 #pragma unroll
@@ -817,28 +858,30 @@ __global__ __launch_bounds__(kThreads) void slot_scan_kernel(const float* __rest
 }
 
 struct SlotPlan {
-  int HD, TC, seg_tiles, nseg, cshift;
+  int HD, TC, seg_rows, nseg, cshift;
   bool has_w;
 };
+
+// Supported head dims: multiples of 16 up to 128.
+inline bool slot_head_dim_ok(int64_t hd) { return hd >= 16 && hd <= 128 && hd % 16 == 0; }
 
 int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype, SlotPlan* pl) {
   if (dtype != HDCM_F32 && dtype != HDCM_BF16) return HDCM_EUNSUPPORTED;
   if (B < 0 || L < 0 || dm <= 0 || H <= 0 || C <= 0 || dm % H) return HDCM_EINVAL;
   const int64_t HD = dm / H;
-  if (HD != 32 && HD != 64 && HD != 96 && HD != 128) return HDCM_EUNSUPPORTED;
+  if (!slot_head_dim_ok(HD)) return HDCM_EUNSUPPORTED;
   const int TC = dtype == HDCM_BF16 ? 64 : 32;
   if (L % C) return HDCM_EINVAL;
+  if (C > ((int64_t)1 << 30)) return HDCM_EUNSUPPORTED;
+  // C dividing TC (a power of two below it): tiles of TC rows hold whole chunks; any other C:
+  // chunk-confined tiles (cshift = 31), ceil(C/TC) per chunk
   int cshift = 31;
-  if (C < TC) {
-    if (TC % C) return HDCM_EUNSUPPORTED;
+  if (C < TC && TC % C == 0) {
     cshift = 0;
     while ((1 << cshift) < C) ++cshift;
-  } else if (C % TC) {
-    return HDCM_EUNSUPPORTED;
   }
   if (B > 65535 || H > 65535) return HDCM_EUNSUPPORTED;
   const int64_t tiles = (L + TC - 1) / TC;
-  const int64_t unit = C > TC ? C / TC : 1;
   int64_t st = hdcm_option_value(HDCM_OPT_SLOT_SEG_TILES);  // 0: automatic
   if (st == 0) {
     const int64_t bh = B * H > 0 ? B * H : 1;
@@ -846,14 +889,21 @@ int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype,
     st = (tiles + want - 1) / want;
     if (st < kMinSegTiles) st = kMinSegTiles;
   }
-  st = (st + unit - 1) / unit * unit;
-  const int64_t cap = (tiles + unit - 1) / unit * unit;
-  if (st > cap) st = cap;
   if (st < 1) st = 1;
+  // segments start on chunk boundaries: whole TC-row tiles (C dividing TC), else whole chunks
+  int64_t seg_rows;
+  if (cshift < 31) {
+    seg_rows = st * TC;
+  } else {
+    const int64_t tpc = (C + TC - 1) / TC;  // tiles per chunk
+    seg_rows = (st + tpc - 1) / tpc * C;
+  }
+  if (L > 0 && seg_rows > L) seg_rows = cshift < 31 ? tiles * TC : L;
+  if (seg_rows < 1) seg_rows = 1;
   pl->HD = (int)HD;
   pl->TC = TC;
-  pl->seg_tiles = (int)st;
-  pl->nseg = (int)((tiles + st - 1) / st);
+  pl->seg_rows = (int)(seg_rows > ((int64_t)1 << 30) ? ((int64_t)1 << 30) : seg_rows);
+  pl->nseg = (int)((L + seg_rows - 1) / seg_rows);
   if (pl->nseg < 1) pl->nseg = 1;
   pl->cshift = cshift;
   pl->has_w = C > TC;
@@ -876,13 +926,13 @@ int launch_state(const void* base, int64_t prs, int64_t k_col, int64_t v_off, co
   if (pl.nseg > 1) {
     HDCM_LAUNCH((slot_state_kernel<T, HD, TC, PHI>), dim3((unsigned)H, pl.nseg - 1, (unsigned)B),
                        dim3(kThreads), 0, s, (const T*)base, prs, (int)k_col, (int)v_off, (int)L,
-                       (const T*)gamma, pl.seg_tiles, pl.nseg, U);
+                       (const T*)gamma, pl.seg_rows, pl.nseg, U);
     const int st = hdcm_launch_status();
     if (st) return st;
   }
   HDCM_LAUNCH((slot_scan_kernel<T>), dim3((HD * HD + kThreads - 1) / kThreads, (unsigned)H, (unsigned)B),
                      dim3(kThreads), 0, s, U, S0, Ain, (const T*)gamma, HD * HD, pl.nseg,
-                     pl.seg_tiles * TC);
+                     pl.seg_rows);
   return hdcm_launch_status();
 }
 
@@ -904,7 +954,7 @@ int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int
 #define HDCM_GATE_LAUNCH(W, P)                                                                              \
   HDCM_LAUNCH((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
                      (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
-                     pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_tiles, \
+                     pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_rows,   \
                      pl.nseg, (T*)out, ors, (int)out_col, S_final, row_stats, stats_ps, (const T*)zb, zrs)
   if (pl.has_w) {
     if (pairs) HDCM_GATE_LAUNCH(true, true);
@@ -952,14 +1002,22 @@ extern "C" int hdcm_slot_state_fwd(const void* projs, int64_t proj_row_stride, i
   if (pl.HD == HDV)                                                                              \
     return launch_state<TT, HDV, true>(projs, proj_row_stride, q_col + dm, dm, gamma, S0, ws, B, L, H, pl, s);
   if (dtype == HDCM_BF16) {
+    HDCM_STATE_CASE(bf16_t, 16)
     HDCM_STATE_CASE(bf16_t, 32)
+    HDCM_STATE_CASE(bf16_t, 48)
     HDCM_STATE_CASE(bf16_t, 64)
+    HDCM_STATE_CASE(bf16_t, 80)
     HDCM_STATE_CASE(bf16_t, 96)
+    HDCM_STATE_CASE(bf16_t, 112)
     HDCM_STATE_CASE(bf16_t, 128)
   } else {
+    HDCM_STATE_CASE(float, 16)
     HDCM_STATE_CASE(float, 32)
+    HDCM_STATE_CASE(float, 48)
     HDCM_STATE_CASE(float, 64)
+    HDCM_STATE_CASE(float, 80)
     HDCM_STATE_CASE(float, 96)
+    HDCM_STATE_CASE(float, 112)
     HDCM_STATE_CASE(float, 128)
   }
 #undef HDCM_STATE_CASE
@@ -996,14 +1054,22 @@ extern "C" int hdcm_slot_gate_fwd(const void* projs, int64_t proj_row_stride, in
                                             gn_b, gn_eps, ws, out, out_row_stride, out_col, S_final, row_stats, \
                                             stats_part_stride, B, L, H, C, pl, s);
   if (dtype == HDCM_BF16) {
+    HDCM_GATE_CASE(bf16_t, 16)
     HDCM_GATE_CASE(bf16_t, 32)
+    HDCM_GATE_CASE(bf16_t, 48)
     HDCM_GATE_CASE(bf16_t, 64)
+    HDCM_GATE_CASE(bf16_t, 80)
     HDCM_GATE_CASE(bf16_t, 96)
+    HDCM_GATE_CASE(bf16_t, 112)
     HDCM_GATE_CASE(bf16_t, 128)
   } else {
+    HDCM_GATE_CASE(float, 16)
     HDCM_GATE_CASE(float, 32)
+    HDCM_GATE_CASE(float, 48)
     HDCM_GATE_CASE(float, 64)
+    HDCM_GATE_CASE(float, 80)
     HDCM_GATE_CASE(float, 96)
+    HDCM_GATE_CASE(float, 112)
     HDCM_GATE_CASE(float, 128)
   }
 #undef HDCM_GATE_CASE
@@ -1052,22 +1118,38 @@ extern "C" int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_
                                            nullptr, 0, B, L, H, C, pl, s);                                  \
   }
   if (dtype == HDCM_BF16) {
+    HDCM_ATTEND_CASE(bf16_t, 16, true)
     HDCM_ATTEND_CASE(bf16_t, 32, true)
+    HDCM_ATTEND_CASE(bf16_t, 48, true)
     HDCM_ATTEND_CASE(bf16_t, 64, true)
+    HDCM_ATTEND_CASE(bf16_t, 80, true)
     HDCM_ATTEND_CASE(bf16_t, 96, true)
+    HDCM_ATTEND_CASE(bf16_t, 112, true)
     HDCM_ATTEND_CASE(bf16_t, 128, true)
+    HDCM_ATTEND_CASE(bf16_t, 16, false)
     HDCM_ATTEND_CASE(bf16_t, 32, false)
+    HDCM_ATTEND_CASE(bf16_t, 48, false)
     HDCM_ATTEND_CASE(bf16_t, 64, false)
+    HDCM_ATTEND_CASE(bf16_t, 80, false)
     HDCM_ATTEND_CASE(bf16_t, 96, false)
+    HDCM_ATTEND_CASE(bf16_t, 112, false)
     HDCM_ATTEND_CASE(bf16_t, 128, false)
   } else {
+    HDCM_ATTEND_CASE(float, 16, true)
     HDCM_ATTEND_CASE(float, 32, true)
+    HDCM_ATTEND_CASE(float, 48, true)
     HDCM_ATTEND_CASE(float, 64, true)
+    HDCM_ATTEND_CASE(float, 80, true)
     HDCM_ATTEND_CASE(float, 96, true)
+    HDCM_ATTEND_CASE(float, 112, true)
     HDCM_ATTEND_CASE(float, 128, true)
+    HDCM_ATTEND_CASE(float, 16, false)
     HDCM_ATTEND_CASE(float, 32, false)
+    HDCM_ATTEND_CASE(float, 48, false)
     HDCM_ATTEND_CASE(float, 64, false)
+    HDCM_ATTEND_CASE(float, 80, false)
     HDCM_ATTEND_CASE(float, 96, false)
+    HDCM_ATTEND_CASE(float, 112, false)
     HDCM_ATTEND_CASE(float, 128, false)
   }
 #undef HDCM_ATTEND_CASE

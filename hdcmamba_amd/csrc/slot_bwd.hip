@@ -299,7 +299,7 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
   HDCM_CHECK_ARG(gn_w && gn_b && dgn_w && dgn_b && ((y && gate && dout && dy && dgate) || rows == 0), HDCM_EINVAL);
   HDCM_CHECK_ARG(rows >= 0 && dm > 0 && H > 0 && dm % H == 0, HDCM_EINVAL);
   const int64_t hd = dm / H;
-  HDCM_CHECK_ARG(hd == 32 || hd == 64 || hd == 96 || hd == 128, HDCM_EUNSUPPORTED);
+  HDCM_CHECK_ARG(hd >= 16 && hd <= 128 && hd % 16 == 0, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(H <= 65535, HDCM_EUNSUPPORTED);
   HDCM_CHECK_ARG(ws != nullptr && ws_bytes >= hdcm_gnorm_gate_bwd_workspace_bytes(dm, H), HDCM_EWORKSPACE);
   HDCM_CHECK_ARG(((uintptr_t)ws & 15u) == 0, HDCM_EALIGN);
@@ -326,9 +326,9 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
                        (float*)ws, rows, (int)dm, nstripe);                                                         \
   }
       if (dtype == HDCM_F32) {
-        HDCM_GNS_CASE(float, 32) HDCM_GNS_CASE(float, 64) HDCM_GNS_CASE(float, 128)
+        HDCM_GNS_CASE(float, 16) HDCM_GNS_CASE(float, 32) HDCM_GNS_CASE(float, 64) HDCM_GNS_CASE(float, 128)
       } else {
-        HDCM_GNS_CASE(bf16_t, 32) HDCM_GNS_CASE(bf16_t, 64) HDCM_GNS_CASE(bf16_t, 128)
+        HDCM_GNS_CASE(bf16_t, 16) HDCM_GNS_CASE(bf16_t, 32) HDCM_GNS_CASE(bf16_t, 64) HDCM_GNS_CASE(bf16_t, 128)
       }
 #undef HDCM_GNS_CASE
       const int st = hdcm_launch_status();
@@ -352,9 +352,11 @@ extern "C" int hdcm_gnorm_gate_bwd(const void* y, int64_t y_row_stride, const vo
                        (int)H);                                                                                     \
   }
     if (dtype == HDCM_F32) {
-      HDCM_GNG_CASE(float, 32) HDCM_GNG_CASE(float, 64) HDCM_GNG_CASE(float, 96) HDCM_GNG_CASE(float, 128)
+      HDCM_GNG_CASE(float, 16) HDCM_GNG_CASE(float, 32) HDCM_GNG_CASE(float, 48) HDCM_GNG_CASE(float, 64)
+      HDCM_GNG_CASE(float, 80) HDCM_GNG_CASE(float, 96) HDCM_GNG_CASE(float, 112) HDCM_GNG_CASE(float, 128)
     } else {
-      HDCM_GNG_CASE(bf16_t, 32) HDCM_GNG_CASE(bf16_t, 64) HDCM_GNG_CASE(bf16_t, 96) HDCM_GNG_CASE(bf16_t, 128)
+      HDCM_GNG_CASE(bf16_t, 16) HDCM_GNG_CASE(bf16_t, 32) HDCM_GNG_CASE(bf16_t, 48) HDCM_GNG_CASE(bf16_t, 64)
+      HDCM_GNG_CASE(bf16_t, 80) HDCM_GNG_CASE(bf16_t, 96) HDCM_GNG_CASE(bf16_t, 112) HDCM_GNG_CASE(bf16_t, 128)
     }
 #undef HDCM_GNG_CASE
     const int st = hdcm_launch_status();

@@ -103,7 +103,8 @@ int hdcm_norm_conv_fwd(const void* x, int64_t x_batch_stride, int64_t x_row_stri
  * d_conv_b [D].  Exact gradients of the forward, including the ln_b terms through the
  * LayerNorm of the zero rows before the sequence start; parameter gradients are summed in
  * a fixed order (deterministic).  ws: hdcm_norm_conv_bwd_workspace_bytes(B, L, D) bytes,
- * 256-byte aligned.  Needs D <= 2048.
+ * 256-byte aligned.  Needs D % (16/elt_size) == 0 and D/(16/elt_size) <= 768 (bf16
+ * D <= 6144, fp32 D <= 3072: the forward's limits).
  * Replaces: FusedNormConv1dFunction.backward -> _fused_norm_conv_bwd_kernel
  *           (hdcmamba/model.py:149-166, kernel model.py:74-124), which omits the ln_b
  *           terms of d_conv_w and d_ln_b and uses bf16-rounded row statistics.
@@ -189,8 +190,9 @@ int hdcm_ssm_bwd(const void* projs, int64_t proj_row_stride, const void* A_log, 
  * NULL): for row r = b*L+t and head h, the pair (sum, sum of squares) of the hd values
  * stored (as rounded) at row_stats[2*(h*stats_part_stride + r)] and the next float;
  * stats_part_stride (in pairs) >= B*L (partial statistics for hdcm_rowln_gemm_stats_fwd).
- * Needs hd in {32,64,96,128}; C a power of two dividing the row tile (64 rows
- * for bf16, 32 for fp32) or a multiple of it; L a multiple of C.
+ * Needs hd a multiple of 16 up to 128, and L a multiple of C (any C >= 1: a C that
+ * neither divides the row tile of 64 rows (bf16) / 32 rows (fp32) nor is a multiple of it
+ * is walked in tiles confined to one chunk each).
  * Replaces: _slot_all_fused launch (hdcmamba/model.py:366-371, kernel
  *           model.py:236-272) and the slot part of _fused_gnorm_gate_cat_kernel
  *           (model.py:375-380, kernel model.py:274-293).
@@ -237,7 +239,7 @@ int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, in
  * values) and sigmoid gate of hdcm_slot_gate_fwd, on `rows` token rows: from y (the slot
  * recurrence's output before the GroupNorm), the gate values and dout, writes dy and dgate
  * (activation dtype) and d gn_w, d gn_b (fp32 [dm], summed in a fixed order).
- * ws: hdcm_gnorm_gate_bwd_workspace_bytes(dm, H) bytes.  hd in {32, 64, 96, 128}.
+ * ws: hdcm_gnorm_gate_bwd_workspace_bytes(dm, H) bytes.  hd a multiple of 16 up to 128.
  * No reference counterpart (model.py:274-295 has no backward).
  */
 size_t hdcm_gnorm_gate_bwd_workspace_bytes(int64_t dm, int64_t H);
@@ -280,7 +282,7 @@ int hdcm_slot_phi_chain(const void* projs, int64_t proj_row_stride, int64_t q_co
  * its chunk's own decayed sum plus gamma^pos S_prev; not read at a chunk start), both fp32
  * and updated; pos = t mod C is the token's offset in its chunk (0 right after a prefill,
  * whose padded length is a multiple of C).  Writes y_ssm to columns [y_col, y_col+ds) and
- * the gated slot output to [g_col, g_col+dm) of out.  Needs hd in {32,64,96,128} and
+ * the gated slot output to [g_col, g_col+dm) of out.  Needs hd a multiple of 16 up to 128 and
  * 16-byte aligned S_prev / S_intra.  With pos_dev
  * non-NULL the offset is read from that device int32 instead of pos, so one captured
  * graph of a decode step serves every position; hdcm_chunk_pos_advance then moves it to

@@ -42,8 +42,11 @@ def test_workspace_sizes():
     assert lib.hdcm_ssm_workspace_bytes(0, 10, 4) == 0
     n = lib.hdcm_slot_workspace_bytes(1, 32768, 1024, 16, 64, _ops.HDCM_BF16)
     assert n > 0 and n % (2 * 16 * 64 * 64 * 4) == 0
-    assert lib.hdcm_slot_workspace_bytes(1, 64, 240, 5, 64, _ops.HDCM_BF16) == 0  # head dim 48
-    assert lib.hdcm_slot_workspace_bytes(1, 96, 256, 4, 48, _ops.HDCM_BF16) == 0  # chunk 48
+    assert lib.hdcm_slot_workspace_bytes(1, 64, 200, 5, 64, _ops.HDCM_BF16) == 0  # head dim 40
+    assert lib.hdcm_slot_workspace_bytes(1, 64, 576, 4, 64, _ops.HDCM_BF16) == 0  # head dim 144
+    assert lib.hdcm_slot_workspace_bytes(1, 64, 240, 5, 64, _ops.HDCM_BF16) > 0   # head dim 48
+    assert lib.hdcm_slot_workspace_bytes(1, 96, 256, 4, 48, _ops.HDCM_BF16) > 0   # chunk 48
+    assert lib.hdcm_slot_workspace_bytes(1, 100, 256, 4, 48, _ops.HDCM_BF16) == 0  # L not a multiple of C
 
 
 P16 = ctypes.c_void_p(16 * 1024)       # aligned non-null stand-ins: never dereferenced,
@@ -110,7 +113,7 @@ def test_slot_validation():
     assert st(*a) == EINVAL
     a = list(base); a[8] = 250  # L not a multiple of C
     assert st(*a) == EINVAL
-    a = list(base); a[11] = 48; a[8] = 96  # chunk 48 neither divides nor is a multiple of 64
+    a = list(base); a[9] = 200; a[10] = 5; a[1] = 3 * 64 + 4 * 200  # head dim 40: not a multiple of 16
     assert st(*a) == EUNSUPPORTED
     a = list(base); a[5] = None
     assert st(*a) == EWORKSPACE
@@ -256,7 +259,7 @@ def test_norm_conv_bwd_validation():
     assert f(*a) == EINVAL
     a = list(base); a[17] = ws_n - 1  # short workspace
     assert f(*a) == EWORKSPACE
-    a = list(base); a[20] = 4096; a[2] = a[5] = a[11] = 4096; a[1] = a[4] = a[10] = 64 * 4096  # D too wide
+    a = list(base); a[20] = 8192; a[2] = a[5] = a[11] = 8192; a[1] = a[4] = a[10] = 64 * 8192  # D too wide
     assert f(*a) == EUNSUPPORTED
     a = list(base); a[20] = 250; a[2] = a[5] = a[11] = 250; a[1] = a[4] = a[10] = 64 * 250
     assert f(*a) == EALIGN
@@ -316,7 +319,7 @@ def test_backward_entry_points_validation():
     assert f(*a) == OK
     a = list(base); a[8] = ws_n - 1
     assert f(*a) == EWORKSPACE
-    a = list(base); a[16] = 240; a[17] = 5  # head dim 48
+    a = list(base); a[16] = 200; a[17] = 5  # head dim 40: not a multiple of 16
     assert f(*a) == EUNSUPPORTED
     a = list(base); a[12] = P16; a[13] = 200  # chain rows shorter than out's block
     assert f(*a) == EINVAL
@@ -341,7 +344,7 @@ def test_backward_entry_points_validation():
     hb = [P16, 256, P16, 256, P16, P16, 1e-5, P16, 256, P16, 256, P16, 256, P16, P16, P16, m, 10, 256, 4, 1, None]
     a = list(hb); a[19] = 5  # dm not a multiple of H
     assert h(*a) == EINVAL
-    a = list(hb); a[18] = 240; a[19] = 5  # head dim 48
+    a = list(hb); a[18] = 200; a[19] = 5  # head dim 40: not a multiple of 16
     assert h(*a) == EUNSUPPORTED
     a = list(hb); a[16] = m - 1
     assert h(*a) == EWORKSPACE

@@ -65,6 +65,30 @@ def test_block_default_heads_hd128(dev, dtype):
     assert_close(y, ref, dtype, f"hd128 {dtype}")
 
 
+@pytest.mark.parametrize("dtype,dm,H,C,L", [
+    (torch.bfloat16, 768, 16, 48, 200),   # hd 48, C 48: one chunk per 64-row tile, left pad 40
+    (torch.float32, 640, 8, 96, 300),     # hd 80, C 96: tiles of 32 rows, three per chunk
+    (torch.bfloat16, 256, 16, 80, 170),   # hd 16, C 80: tiles of 64 + 16 rows per chunk
+    (torch.bfloat16, 896, 8, 64, 130),    # hd 112
+])
+def test_block_general_head_dims_and_chunks(dev, dtype, dm, H, C, L):
+    """Head dims that are multiples of 16 but not of 32 and chunk sizes that neither divide
+    the row tile nor are multiples of it, through the whole block (padding, SSM, slot + gate,
+    the out_proj fold in bf16)."""
+    print("block general", dtype, dm, H, C, L, flush=True)
+    from hdcmamba_amd import HdcMamba9v3Block
+    from cfgs import reinit_block_
+
+    torch.manual_seed(dm + C)
+    blk = reinit_block_(HdcMamba9v3Block(dm, 64, H, C), seed=dm + C, decays_uniform=True).eval().to(dtype)
+    x = torch.randn(2, L, dm, generator=torch.Generator().manual_seed(L)).to(dtype)
+    ref = oracle.block_forward(_sd(blk), x, oracle_cfg(blk))
+    with torch.no_grad():
+        y, _ = blk.to(dev)(x.to(dev))
+    print("max rel", max_rel(y, ref), flush=True)
+    assert_close(y, ref, dtype, f"dm={dm} H={H} C={C}")
+
+
 def test_model_and_lm_small(dev):
     """2-layer LM (d_model 768, heads 12) at B=2, L=512 through embedding, blocks, norms, tied head."""
     print("lm small", flush=True)

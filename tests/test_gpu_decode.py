@@ -36,6 +36,9 @@ BLOCK_CASES = [
     (torch.float32, 1, 512, 64, 8, 32, 64, 40),    # hd 64, aligned prefill
     (torch.bfloat16, 2, 512, 128, 8, 64, 130, 70),  # hd 64, prefill padded by 62
     (torch.bfloat16, 1, 768, 64, 8, 64, 64, 66),   # hd 96
+    (torch.bfloat16, 2, 768, 64, 16, 48, 100, 60),  # hd 48, C 48 (chunk-confined tiles), padded prefill
+    (torch.float32, 1, 320, 64, 4, 80, 160, 90),   # hd 80, C 80 > TC (fp32 tile 32)
+    (torch.bfloat16, 1, 256, 64, 16, 96, 96, 100),  # hd 16, C 96: tiles of 64 + 32 rows
 ]
 
 

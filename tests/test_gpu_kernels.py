@@ -43,6 +43,12 @@ def test_norm_conv_wide_rows_bf16(dev, D, L):
     test_norm_conv(dev, torch.bfloat16, D, L)
 
 
+@pytest.mark.parametrize("D,L", [(4096, 33), (6144, 18)])
+def test_norm_conv_backward_wide_bf16(dev, D, L):
+    """bf16 rows up to the forward's 6144 columns through the shared-row backward kernel."""
+    test_norm_conv_backward(dev, torch.bfloat16, 1, L, D)
+
+
 def test_norm_conv_batch_strided(dev):
     """A batch-strided view (rows 3.. of a longer buffer) is read through its strides."""
     g = torch.Generator().manual_seed(7)
@@ -203,6 +209,21 @@ SLOT_CASES = [
     (torch.float32, 1, 256, 512, 4, 16),     # hd 128, C < TC
     (torch.bfloat16, 2, 320, 1024, 8, 64),   # hd 128 (d_model 1024 with the default 8 heads)
     (torch.bfloat16, 1, 512, 512, 4, 128),   # hd 128, C > TC
+    # head dims that are multiples of 16 but not of 32 (zero-padded contraction columns)
+    (torch.bfloat16, 1, 256, 256, 16, 64),   # hd 16
+    (torch.float32, 2, 192, 256, 16, 64),    # hd 16
+    (torch.bfloat16, 2, 320, 768, 16, 64),   # hd 48 (d_model 768 with 16 heads)
+    (torch.float32, 1, 256, 384, 8, 32),     # hd 48
+    (torch.bfloat16, 1, 384, 640, 8, 128),   # hd 80, C > TC
+    (torch.float32, 1, 256, 320, 4, 16),     # hd 80, C < TC
+    (torch.bfloat16, 1, 256, 896, 8, 64),    # hd 112
+    # chunks that neither divide the row tile nor are multiples of it (chunk-confined tiles)
+    (torch.bfloat16, 1, 288, 256, 4, 48),    # C 48 < TC: one chunk per tile, 16 rows idle
+    (torch.bfloat16, 2, 384, 512, 8, 96),    # C 96 > TC: tiles of 64 + 32 rows per chunk
+    (torch.float32, 1, 240, 256, 4, 48),     # fp32 (TC 32): tiles of 32 + 16 rows per chunk
+    (torch.float32, 1, 240, 256, 4, 24),     # fp32 C 24 < TC
+    (torch.bfloat16, 1, 250, 256, 4, 50),    # C not a multiple of 16
+    (torch.bfloat16, 1, 1000, 256, 4, 100),  # several segments of whole chunks
 ]
 
 
@@ -260,6 +281,9 @@ ATTEND_CASES = [
     (torch.bfloat16, 1, 256, 768, 8, 128),   # hd 96
     (torch.bfloat16, 1, 256, 1024, 8, 64),   # hd 128
     (torch.float32, 1, 128, 512, 4, 32),     # hd 128
+    (torch.bfloat16, 1, 192, 384, 8, 48),    # hd 48, C 48: chunk-confined tiles
+    (torch.float32, 1, 160, 320, 4, 80),     # hd 80, C 80 > TC, not a multiple of it
+    (torch.bfloat16, 1, 192, 256, 16, 96),   # hd 16, C 96
 ]
 
 
@@ -304,22 +328,29 @@ def test_slot_attend(dev, dtype, B, L, dm, H, C, phi, reverse):
     assert err <= lim, ("chain", err)
 
 
-def test_slot_segments_option(dev):
-    """Different segment lengths (state pre-pass on/off) give the same result."""
-    dm, ds, H, C, B, L = 256, 64, 4, 64, 1, 1024
-    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, torch.float32, seed=3)
+@pytest.mark.parametrize("C,L", [(64, 1024), (48, 960), (96, 960), (80, 960)])
+def test_slot_segments_option(dev, C, L):
+    """Different segment lengths (state pre-pass on/off) give the same result, and the
+    oracle's; for chunks that do not divide the row tile the segments hold whole chunks."""
+    dm, ds, H, B = 256, 64, 4, 1
+    _say("slot segments", C, L)
+    projs, gamma, gn_w, gn_b = slot_inputs(B, L, dm, ds, H, torch.float32, seed=3 + C)
     outs = []
-    for st in (1, 2, 16):
+    for st in (1, 2, 3, 16):
         with _ops.option("slot_seg_tiles", st):
             outs.append(_run_slot(dev, projs, gamma, gn_w, gn_b, dm, ds, H, C)[0])
     for o in outs[1:]:
         assert_close(o, outs[0], torch.float32, "segment invariance")
+    y, _ = oracle.slot_chunked(projs, gamma, dm, ds, H, C, torch.float32)
+    ref = oracle.gnorm_gate(y, projs[..., 3 * ds + 3 * dm:], gn_w, gn_b, H)
+    assert_close(outs[0][..., ds:], ref, torch.float32, "slot+gate")
 
 
-def test_slot_unsupported_head_dim(dev):
-    projs, gamma, gn_w, gn_b = slot_inputs(1, 64, 240, 64, 5, torch.bfloat16)  # hd 48
+@pytest.mark.parametrize("dm,H", [(200, 5), (576, 4)])  # hd 40 (not a multiple of 16), hd 144
+def test_slot_unsupported_head_dim(dev, dm, H):
+    projs, gamma, gn_w, gn_b = slot_inputs(1, 64, dm, 64, H, torch.bfloat16)
     with pytest.raises(_ops.HdcmError):
-        _run_slot(dev, projs, gamma, gn_w, gn_b, 240, 64, 5, 64)
+        _run_slot(dev, projs, gamma, gn_w, gn_b, dm, 64, H, 64)
 
 
 # ----------------------------------------------------------------------------- skinny decode GEMM
@@ -530,10 +561,12 @@ def test_fused_out_proj_matches_unfused(dev):
 # ----------------------------------------------------------------------------- norm_conv backward
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,L,D", [(2, 1, 256), (2, 5, 256), (1, 300, 1024), (2, 700, 768), (1, 64, 2048),
-                                   (3, 131, 512), (1, 70, 1280), (2, 40, 1536)])
+                                   (3, 131, 512), (1, 70, 1280), (2, 40, 1536),
+                                   (2, 37, 3072), (1, 20, 2560)])  # rows shared by a workgroup's waves
 def test_norm_conv_backward(dev, dtype, B, L, D):
     """FusedNormConv1dFunction's backward against autograd through the oracle (fp64 for fp32
-    inputs): dx elementwise, the parameter gradients (sums over B*L rows) normwise."""
+    inputs): dx elementwise, the parameter gradients (sums over B*L rows) normwise.  D above
+    2048 takes the kernel whose four waves share each row."""
     from hdcmamba_amd import FusedNormConv1dFunction
 
     _say("norm_conv bwd", dtype, B, L, D)

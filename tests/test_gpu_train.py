@@ -192,11 +192,13 @@ def test_ssm_backward(dev, dtype):
 @pytest.mark.parametrize("dtype,H,dm,B,L", [(torch.float32, 4, 256, 2, 100), (torch.bfloat16, 4, 256, 2, 100),
                                             (torch.bfloat16, 8, 256, 2, 100), (torch.float32, 2, 256, 2, 100),
                                             (torch.bfloat16, 8, 768, 2, 100), (torch.float32, 8, 768, 1, 70),
-                                            (torch.bfloat16, 4, 512, 1, 2600), (torch.float32, 16, 1024, 1, 2051)])
+                                            (torch.bfloat16, 4, 512, 1, 2600), (torch.float32, 16, 1024, 1, 2051),
+                                            (torch.bfloat16, 16, 768, 2, 90), (torch.float32, 16, 256, 2, 90),
+                                            (torch.bfloat16, 8, 640, 1, 70)])
 def test_gnorm_gate_backward(dev, dtype, H, dm, B, L):
     """dy, d gate, d gn_w, d gn_b of the per-token GroupNorm + gate against autograd through
-    the oracle: head dims 64, 32 and 128 (row-stripe kernel; one partial stripe at dm 256,
-    more tokens than the 2048 waves at L 2600 and 2051) and 96 (per-head kernel)."""
+    the oracle: head dims 64, 32, 128 and 16 (row-stripe kernel; one partial stripe at dm 256,
+    more tokens than the 2048 waves at L 2600 and 2051) and 96, 48, 80 (per-head kernel)."""
     from hdcmamba_amd import _ops
 
     _say("gnorm gate bwd", dtype, H, dm, B, L)
@@ -220,25 +222,28 @@ def test_gnorm_gate_backward(dev, dtype, H, dm, B, L):
         assert err <= lim, (name, err)
 
 
-@pytest.mark.parametrize("dtype,L", [(torch.float32, 192), (torch.bfloat16, 192), (torch.float32, 100)])
-def test_differentiable_mixer_block(dev, dtype, L):
+@pytest.mark.parametrize("dtype,L,dm,H,C", [(torch.float32, 192, 256, 4, 64), (torch.bfloat16, 192, 256, 4, 64),
+                                            (torch.float32, 100, 256, 4, 64),
+                                            (torch.bfloat16, 144, 384, 8, 48),   # hd 48, C 48
+                                            (torch.float32, 160, 320, 4, 80)])  # hd 80, C 80
+def test_differentiable_mixer_block(dev, dtype, L, dm, H, C):
     """A block with differentiable_mixer: gradients of every parameter but decay_log and of
     the input against autograd through the oracle block with mixer_grad (the full derivative
     of the intended forward, gamma held constant)."""
     from hdcmamba_amd import HdcMamba9v3Block
 
-    _say("differentiable mixer", dtype, L)
-    cfg = oracle.BlockCfg(256, 64, 4, 64)
+    _say("differentiable mixer", dtype, L, dm, H, C)
+    cfg = oracle.BlockCfg(dm, 64, H, C)
     torch.manual_seed(2)
-    blk = reinit_block_(HdcMamba9v3Block(256, 64, 4, 64, differentiable_mixer=True), seed=51,
+    blk = reinit_block_(HdcMamba9v3Block(dm, 64, H, C, differentiable_mixer=True), seed=51,
                         decays_uniform=True).to(dtype).train()
     with torch.no_grad():  # non-trivial LayerNorm / GroupNorm affine parameters
         for t in (blk.norm.weight, blk.group_norm.weight):
             t.add_(0.1 * torch.randn(t.shape, generator=torch.Generator().manual_seed(52)).to(dtype))
         for t in (blk.norm.bias, blk.group_norm.bias):
             t.add_(0.05 * torch.randn(t.shape, generator=torch.Generator().manual_seed(53)).to(dtype))
-    x = torch.randn(2, L, 256, generator=torch.Generator().manual_seed(54)).to(dtype)
-    R = torch.randn(2, L, 256, generator=torch.Generator().manual_seed(55))
+    x = torch.randn(2, L, dm, generator=torch.Generator().manual_seed(54)).to(dtype)
+    R = torch.randn(2, L, dm, generator=torch.Generator().manual_seed(55))
     sd = {k: v.detach().clone() for k, v in blk.state_dict().items()}
     sd["gamma_buf"] = torch.exp(-F.softplus(sd["decay_log"]))
     for v in sd.values():
