@@ -147,22 +147,30 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(
 // bytes, and stages it in a private LDS slab, from which the B fragments are read.  Every
 // lane issues the same number of loads (pieces past the wave's range re-read one inside the
 // row and are never used), so all loads are in flight before the first wait.
+// NCOL (16 or 8) output columns per workgroup: with 8, a workgroup streams 8 weight rows and
+// the MFMA's other 8 columns repeat them (their outputs are not stored), which doubles the
+// workgroups of a narrow output (the d_model 2048 out_proj: 256 instead of 128, every CU
+// streaming) at the cost of reading the activation rows twice as often from L2.
 constexpr int kLdsWaves = 8;
 constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kWideN = 2048;
+// outputs of the LDS kernel up to this width use 8-column workgroups (HDCM_OPT_SKINNY_COLS8_MAX_N)
+inline bool cols8(int N) { return N <= hdcm_option_value(HDCM_OPT_SKINNY_COLS8_MAX_N); }
 
-template <int STEPS, bool BIAS, bool RES, bool LN = false>
+template <int STEPS, bool BIAS, bool RES, bool LN = false, int NCOL = 16>
 __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
     const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
     const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
     bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K, float eps = 0.f) {
+  static_assert(NCOL == 16 || NCOL == 8, "columns per workgroup");
   constexpr int PITCH = STEPS * 32 + 8;  // slab row pitch (elements): +16 bytes staggers the banks
-  __shared__ __attribute__((aligned(16))) bf16_t slab[kLdsWaves][16 * PITCH];
+  constexpr int NLD = (NCOL * 4 * STEPS + kWave - 1) / kWave;  // 16-byte weight loads per lane
+  __shared__ __attribute__((aligned(16))) bf16_t slab[kLdsWaves][NCOL * PITCH];
   __shared__ float part[kLdsWaves][16][17];
   __shared__ float lnst[LN ? kLdsWaves : 1][16][3];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int l16 = lane & 15, g = lane >> 4;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * NCOL;
   const int nsteps = K / 32;
   const int base = nsteps / kLdsWaves, extra = nsteps % kLdsWaves;
   const int my = base + (w < extra ? 1 : 0);
@@ -171,18 +179,25 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   auto step_of = [&](int s) { return min(s0 + max(min(s, my - 1), 0), nsteps - 1); };
 
   // the epilogue's bias and residual value, loaded now so the epilogue waits for nothing
+  // (thread tid < 16*NCOL: row tid / NCOL, column tid % NCOL)
   float pre = 0.f;
-  if (tid < 256 && tid / 16 < M && n0 + tid % 16 < N) {
-    if (BIAS) pre += bf2f(bias[n0 + tid % 16]);
-    if (RES) pre += bf2f(res[(int64_t)(tid / 16) * r_rs + n0 + tid % 16]);
+  if (tid < 16 * NCOL && tid / NCOL < M && n0 + tid % NCOL < N) {
+    if (BIAS) pre += bf2f(bias[n0 + tid % NCOL]);
+    if (RES) pre += bf2f(res[(int64_t)(tid / NCOL) * r_rs + n0 + tid % NCOL]);
   }
-  uint4 raw[STEPS];
+  // piece idx of the wave's NCOL rows x STEPS steps x 4 sixteen-byte quarters; indices past
+  // them (NCOL*STEPS not a multiple of 16) re-read the last piece and are not staged
+  auto piece = [&](int i, int& r, int& st, int& q) {
+    const int idx = min(kWave * i + lane, NCOL * 4 * STEPS - 1);
+    r = idx / (4 * STEPS), st = (idx / 4) % STEPS, q = idx % 4;
+  };
+  uint4 raw[NLD];
 #pragma unroll
-  for (int i = 0; i < STEPS; ++i) {
-    const int idx = kWave * i + lane;
-    const int r = idx / (4 * STEPS), s = (idx / 4) % STEPS, q = idx % 4;
+  for (int i = 0; i < NLD; ++i) {
+    int r, st, q;
+    piece(i, r, st, q);
     const int n = min(n0 + r, N - 1);  // rows past N re-read row N-1 (outputs not stored)
-    raw[i] = *reinterpret_cast<const uint4*>(W + (int64_t)n * w_rs + 32 * step_of(s) + 8 * q);
+    raw[i] = *reinterpret_cast<const uint4*>(W + (int64_t)n * w_rs + 32 * step_of(st) + 8 * q);
   }
   const int am = l16 < M ? l16 : 0;  // rows past M read row 0 (outputs not stored)
   Frag<bf16_t> fa[STEPS];
@@ -191,19 +206,20 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
     fa[s].v = *reinterpret_cast<const bf16x8_t*>(A + (int64_t)am * a_rs + 32 * step_of(s) + 8 * g);
   bf16_t* sl = slab[w];
 #pragma unroll
-  for (int i = 0; i < STEPS; ++i) {
-    const int idx = kWave * i + lane;
-    const int r = idx / (4 * STEPS), s = (idx / 4) % STEPS, q = idx % 4;
-    *reinterpret_cast<uint4*>(sl + r * PITCH + 32 * s + 8 * q) = raw[i];
+  for (int i = 0; i < NLD; ++i) {
+    int r, st, q;
+    piece(i, r, st, q);
+    if (kWave * i + lane < NCOL * 4 * STEPS) *reinterpret_cast<uint4*>(sl + r * PITCH + 32 * st + 8 * q) = raw[i];
   }
   __syncthreads();
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   float c1 = 0.f, c2 = 0.f, w1 = 0.f;
+  const int br = l16 % NCOL;  // B column l16 reads slab row l16 mod NCOL
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     if (s < my) {
       Frag<bf16_t> b;
-      b.v = *reinterpret_cast<const bf16x8_t*>(sl + l16 * PITCH + 32 * s + 8 * g);
+      b.v = *reinterpret_cast<const bf16x8_t*>(sl + br * PITCH + 32 * s + 8 * g);
       acc = mma(fa[s], b, acc);
       if constexpr (LN) ln_sums(fa[s], b, c1, c2, w1);
     }
@@ -213,8 +229,8 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
   __syncthreads();
-  if (tid < 256) {
-    const int m = tid / 16, nn = tid % 16, n = n0 + nn;
+  if (tid < 16 * NCOL) {
+    const int m = tid / NCOL, nn = tid % NCOL, n = n0 + nn;
     float v = 0.f;
 #pragma unroll
     for (int k = 0; k < kLdsWaves; ++k) v += part[k][m][nn];
@@ -225,24 +241,33 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   }
 }
 
-template <int STEPS>
-void launch_lds(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
-                int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
-  const dim3 grid((unsigned)((N + 15) / 16));
+template <int STEPS, int NCOL>
+void launch_lds_cols(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
+                     int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
+  const dim3 grid((unsigned)((N + NCOL - 1) / NCOL));
   const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
   bf16_t* o = (bf16_t*)out;
   if (bias && res)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, true, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
+                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (bias)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, false, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
+                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else if (res)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt, w_rs,
-                       bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
+                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
   else
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, false>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
-                       w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, false, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs,
+                wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+}
+
+template <int STEPS>
+void launch_lds(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
+                int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
+  if (cols8(N))
+    launch_lds_cols<STEPS, 8>(A, a_rs, W, w_rs, bias, res, r_rs, out, o_rs, M, N, K, s);
+  else
+    launch_lds_cols<STEPS, 16>(A, a_rs, W, w_rs, bias, res, r_rs, out, o_rs, M, N, K, s);
 }
 
 template <int STEPS>
@@ -269,9 +294,17 @@ template <int STEPS, bool WIDE>
 void launch_ln(const bf16_t* c, int64_t c_rs, const bf16_t* W, int64_t w_rs, const bf16_t* res, int64_t r_rs,
                bf16_t* out, int64_t o_rs, int M, int N, int K, float eps, hipStream_t s) {
   const dim3 grid((unsigned)((N + 15) / 16));
-  if constexpr (WIDE)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
-                       w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
+  // narrow wide-kernel outputs (up to 4096 columns by default, e.g. the d_model 2048
+  // out_proj): 8 columns per workgroup, so 2 workgroups per 16 columns stream the weight
+  if constexpr (WIDE) {
+    if (cols8(N))
+      HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true, 8>), dim3((unsigned)((N + 7) / 8)),
+                  dim3(kLdsThreads), 0, s, c, c_rs, W, w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K,
+                  eps);
+    else
+      HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
+                  w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
+  }
   else
     HDCM_LAUNCH((skinny_gemm_kernel<STEPS, false, true, true>), grid, dim3(kThreads), 0, s, c, c_rs, W,
                        w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);

@@ -74,11 +74,20 @@ int hdcm_timed_launch_count(void);
  *    (0 forces that path).  Results do not depend on it.
  *  HDCM_OPT_SLOT_SEG_TILES (env HDCM_SLOT_SEG_TILES, default 0 = automatic): row tiles per
  *    segment of the slot kernels.  Results do not depend on it beyond fp32 rounding.
+ *  HDCM_OPT_SKINNY_COLS8_MAX_N (env HDCM_SKINNY_COLS8_MAX_N, default 4096): skinny GEMM
+ *    outputs (hdcm_skinny_gemm_fwd, hdcm_rowln_gemm_fwd at <= 16 rows) of 2048 up to this
+ *    many columns run 8 output columns per workgroup instead of 16 (0 switches it off).
+ *    Results do not depend on it.
  * hdcm_set_option returns HDCM_EINVAL for an unknown option or a value out of range
- * (both take 0 .. 2^20); hdcm_get_option returns the current value (0 for an unknown one).
+ * (0 .. 2^20, the last one 0 .. 2^30); hdcm_get_option returns the current value (0 for an
+ * unknown one).
  * No counterpart in the reference (its launch table, model.py:12-19, is fixed).
  */
-typedef enum { HDCM_OPT_SSM_SPIN_ROUNDS = 1, HDCM_OPT_SLOT_SEG_TILES = 2 } hdcm_option;
+typedef enum {
+  HDCM_OPT_SSM_SPIN_ROUNDS = 1,
+  HDCM_OPT_SLOT_SEG_TILES = 2,
+  HDCM_OPT_SKINNY_COLS8_MAX_N = 3
+} hdcm_option;
 int hdcm_set_option(int option, int value);
 int hdcm_get_option(int option);
 

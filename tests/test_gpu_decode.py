@@ -60,6 +60,37 @@ def test_block_prefill_then_steps(dev, dtype, B, dm, ds, H, C, n_pre, n_dec):
     assert st.pos == (n_pre + (C - n_pre % C) % C + n_dec) % C
 
 
+@pytest.mark.parametrize("B,n_pre,n_dec", [(2, 8192, 32), (16, 8192, 8)])
+def test_block_c5_width_prefill_then_steps(dev, B, n_pre, n_dec):
+    """A block of the 48-layer d_model 2048 decode workload (32 heads, d_state 128, chunk 64)
+    against the oracle: an 8192-row prefill, then single-token steps.  At B=2 the slot kernels
+    cut each sequence into segments and the prefill's out_proj is the GEMM with the folded
+    LayerNorm; at B=16 (B*H = 512 workgroups) every (sequence, head) is one segment walked
+    from row 0 with no state pre-pass, and the prefill takes the LayerNorm kernel and the
+    library out_proj."""
+    from hdcmamba_amd import _ops
+
+    dm, ds, H, C = 2048, 128, 32, 64
+    dtype = torch.bfloat16
+    _say("c5-width block decode", B, n_pre, n_dec)
+    lib = _ops.lib()
+    nseg = lib.hdcm_slot_workspace_bytes(B, n_pre, dm, H, C, _ops.HDCM_BF16) // (2 * B * H * 64 * 64 * 4)
+    assert (nseg == 1) == (B == 16), nseg
+    blk = _block(dm, ds, H, C, dtype, seed=2048 + B)
+    x = torch.randn(B, n_pre + n_dec, dm, generator=torch.Generator().manual_seed(B)).to(dtype)
+    ref = oracle.block_forward_stream(_sd(blk), x, oracle_cfg(blk), n_pre)
+    blk = blk.to(dev)
+    xd = x.to(dev)
+    with torch.no_grad():
+        y0, st = blk.prefill(xd[:, :n_pre])
+        ys = [blk.step(xd[:, n_pre + t].contiguous(), st) for t in range(n_dec)]
+    _say("  prefill max rel", max_rel(y0, ref[:, :n_pre]))
+    assert_close(y0, ref[:, :n_pre], dtype, "prefill rows")
+    got = torch.stack(ys, 1)
+    _say("  decode max rel", max_rel(got, ref[:, n_pre:]))
+    assert_close(got, ref[:, n_pre:], dtype, "decode rows")
+
+
 def test_steps_from_empty_state_equal_forward(dev):
     """Token-by-token from the empty state reproduces the chunked forward of an aligned
     sequence (both start their chunk grid at row 0)."""

@@ -391,6 +391,39 @@ def test_skinny_gemm(dev, M, N, K, bias, res):
     assert (err <= 2 ** -8 * ref.abs() + 1e-3).all(), f"max err {err.max().item()}"
 
 
+@pytest.mark.parametrize("M,N,K,bias,res,ln", [
+    (16, 2048, 2176, False, True, True),    # the d_model 2048 decode out_proj (LayerNorm folded)
+    (16, 2048, 2176, False, True, False),
+    (16, 8576, 2048, True, False, False),   # its in_proj
+    (9, 2050, 1024, False, True, False),    # ragged last workgroup
+    (9, 2056, 1024, False, True, True),     # 16-column tiles: the last one half full
+    (3, 4100, 96, True, True, False),
+])
+def test_skinny_columns_per_workgroup(dev, M, N, K, bias, res, ln):
+    """8 output columns per workgroup (the MFMA's other 8 columns repeat them) give the same
+    bits as 16: each output column's dot product runs in the same order either way."""
+    _say("skinny cols", M, N, K, bias, res, ln)
+    g = torch.Generator().manual_seed(M + N + K)
+    A = (1.5 * torch.randn(M, K, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev) if bias else None
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev) if res else None
+    outs = []
+    for cols8_max_n in (0, 1 << 30):
+        with _ops.option("skinny_cols8_max_n", cols8_max_n):
+            outs.append(_ops.rowln_gemm(A, W, r) if ln else _ops.skinny_linear(A, W, b, r))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = torch.nn.functional.layer_norm(A.float().cpu(), (K,), eps=1e-5) if ln else A.float().cpu()
+    ref = ref @ W.float().cpu().t()
+    if bias:
+        ref = ref + b.float().cpu()
+    if res:
+        ref = ref + r.float().cpu()
+    err = (outs[1].float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
+
+
 def test_skinny_gemm_in_place_residual(dev):
     """out may be the residual buffer itself."""
     g = torch.Generator().manual_seed(3)
