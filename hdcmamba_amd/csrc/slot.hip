@@ -347,8 +347,11 @@ __device__ __forceinline__ void zero_contraction_pad(T* sm, int tid) {
 // epilogue (else y itself is stored).  CHAIN (without EPI): each stored value is multiplied by
 // phi'(z) = 1 (z > 0) else exp(z), z read from zb at the output's own row and column (zb has
 // the output's column layout, row stride zrs) — the feature map's chain rule of a gradient
-// pass.  k, v and the gate start k_off, v_off, g_off columns after q in each row.
-template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI, bool CHAIN = false>
+// pass.  k, v and the gate start k_off, v_off, g_off columns after q in each row.  CONF: tiles
+// are chunk-confined (a C that neither divides TC nor is a multiple of it); otherwise every
+// tile but a segment's last has TC rows, and the loop steps by the constant TC.
+template <typename T, int HD, int TC, bool HAS_W, bool PAIRS, bool PHI, bool EPI, bool CHAIN = false,
+          bool CONF = false>
 __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerEU)) void slot_gate_kernel(
     const T* __restrict__ projs, int64_t prs, int q_col, int k_off, int v_off, int g_off, int L, int C, int cshift,
     const T* __restrict__ gamma, const T* __restrict__ gn_w, const T* __restrict__ gn_b,
@@ -377,14 +380,17 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
     gnw_raw = gn_w[h * HD + tid % HD];
     gnb_raw = gn_b[h * HD + tid % HD];
   }
-  // cshift >= 31: tiles are chunk-confined (C does not divide TC), so every pair in a tile
-  // shares a chunk; otherwise tiles hold TC/C whole chunks
+  // cshift >= 31: C >= TC or tiles are chunk-confined (CONF), so every pair in a tile shares
+  // a chunk; otherwise tiles hold TC/C whole chunks
   const bool one_chunk = cshift >= 31;
   const int64_t rowbase = (int64_t)b * L;
   const int p_begin = seg * seg_rows;
   const int p_end = min(L, p_begin + seg_rows);
-  // rows of the tile starting at p (p_end and chunk ends are tile ends)
-  auto tile_len = [&](int p) { return one_chunk ? min(min(TC, p_end - p), C - p % C) : min(TC, p_end - p); };
+  // rows of the tile starting at p (p_end, and with CONF chunk ends, are tile ends)
+  auto tile_len = [&](int p) {
+    if constexpr (CONF) return min(min(TC, p_end - p), C - p % C);
+    else return min(TC, p_end - p);
+  };
   const T* colbase = projs + q_col + h * HD;
   // the gate (EPI), or the chain rule's z (CHAIN: same positions as the output)
   const T* gatebase = CHAIN ? zb + out_col + h * HD : colbase + g_off;
@@ -451,7 +457,8 @@ __global__ __launch_bounds__(kThreads, HD > 64 ? 1 : (HAS_W ? 2 : kGateWavesPerE
   }
   zero_contraction_pad<T, HD, TC>(sm, tid);  // ordered before every read by the loop's barriers
 
-  for (int p = p_begin, tlen = tile_len(p_begin); p < p_end; p += tlen, tlen = p < p_end ? tile_len(p) : 0) {
+  for (int p = p_begin; p < p_end; p += CONF ? tile_len(p) : TC) {
+    const int tlen = tile_len(p);
     __syncthreads();
     stage_tile<T, HD, TC, 0, 3, false, PHI>(raw, sm, tlen, lg2, tid);
     // S_eff^T for this tile: gamma*W + gamma^(p-cs)*A (A alone when C divides TC).
@@ -860,6 +867,7 @@ __global__ __launch_bounds__(kThreads) void slot_scan_kernel(const float* __rest
 struct SlotPlan {
   int HD, TC, seg_rows, nseg, cshift;
   bool has_w;
+  bool conf;  // chunk-confined tiles: C neither divides TC nor is a multiple of it
 };
 
 // Supported head dims: multiples of 16 up to 128.
@@ -907,6 +915,7 @@ int slot_plan(int64_t B, int64_t L, int64_t dm, int64_t H, int64_t C, int dtype,
   if (pl->nseg < 1) pl->nseg = 1;
   pl->cshift = cshift;
   pl->has_w = C > TC;
+  pl->conf = cshift >= 31 && C % TC != 0;
   if (pl->nseg > 65535 || L > ((int64_t)1 << 30)) return HDCM_EUNSUPPORTED;
   return HDCM_OK;
 }
@@ -951,17 +960,21 @@ int launch_gate(const void* base, int64_t prs, int64_t q_col, int64_t k_off, int
   // (with CHAIN the z rows must allow the same 16-byte runs)
   const bool pairs = sizeof(T) == 2 && ((uintptr_t)out % 16) == 0 && out_col % 8 == 0 && ors % 8 == 0 &&
                      (!CHAIN || (((uintptr_t)zb % 16) == 0 && zrs % 8 == 0));
-#define HDCM_GATE_LAUNCH(W, P)                                                                              \
-  HDCM_LAUNCH((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN>), grid, dim3(kThreads), 0, s,    \
+#define HDCM_GATE_LAUNCH(W, P, CF)                                                                          \
+  HDCM_LAUNCH((slot_gate_kernel<T, HD, TC, W, P, PHI, EPI, CHAIN, CF>), grid, dim3(kThreads), 0, s,    \
                      (const T*)base, prs, (int)q_col, (int)k_off, (int)v_off, (int)g_off, (int)L, (int)C,  \
                      pl.cshift, (const T*)gamma, (const T*)gn_w, (const T*)gn_b, gn_eps, Ain, pl.seg_rows,   \
                      pl.nseg, (T*)out, ors, (int)out_col, S_final, row_stats, stats_ps, (const T*)zb, zrs)
-  if (pl.has_w) {
-    if (pairs) HDCM_GATE_LAUNCH(true, true);
-    else HDCM_GATE_LAUNCH(true, false);
+  // chunk-confined tiles (rare chunk sizes) run with the 8-byte output runs only
+  if (pl.conf) {
+    if (pl.has_w) HDCM_GATE_LAUNCH(true, false, true);
+    else HDCM_GATE_LAUNCH(false, false, true);
+  } else if (pl.has_w) {
+    if (pairs) HDCM_GATE_LAUNCH(true, true, false);
+    else HDCM_GATE_LAUNCH(true, false, false);
   } else {
-    if (pairs) HDCM_GATE_LAUNCH(false, true);
-    else HDCM_GATE_LAUNCH(false, false);
+    if (pairs) HDCM_GATE_LAUNCH(false, true, false);
+    else HDCM_GATE_LAUNCH(false, false, false);
   }
 #undef HDCM_GATE_LAUNCH
   return hdcm_launch_status();
