@@ -268,7 +268,7 @@ class _Timer:
 timer = _Timer()
 
 # launch options of the library (hdcm_set_option)
-OPTIONS = {"ssm_spin_rounds": 1, "slot_seg_tiles": 2, "skinny_cols8_max_n": 3}
+OPTIONS = {"ssm_spin_rounds": 1, "slot_seg_tiles": 2, "skinny_cols8_max_n": 3, "skinny_fold_tail": 4}
 
 
 class option:
@@ -276,7 +276,9 @@ class option:
     ``with _ops.option("slot_seg_tiles", 8): ...``.  ssm_spin_rounds = polling rounds of the
     scan's look-back before it computes a missing total itself (0 forces that path);
     slot_seg_tiles = row tiles per slot segment (0 = automatic); skinny_cols8_max_n = widest
-    skinny-GEMM output run with 8 columns per workgroup (0 = never).  Launches read the value
+    skinny-GEMM output run with 8 columns per workgroup (0 = never); skinny_fold_tail = 1 runs
+    the skinny GEMM's tiles past one round of resident workgroups as second tiles of the first
+    workgroups (0 = a second round).  Launches read the value
     current when they are issued (a recorded graph keeps the value of its capture)."""
 
     def __init__(self, name, value):

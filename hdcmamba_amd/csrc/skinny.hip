@@ -15,6 +15,8 @@
 // A (the 16 activation rows, a few tens of KB) is read from L2.  The partial 16x16 tiles are
 // summed through LDS and the epilogue adds bias and residual (loaded at the start, so no load
 // waits behind the MFMAs) in fp32 and rounds once to bf16.
+#include <atomic>
+
 #include "hdcm_common.h"
 
 using namespace hdcm;
@@ -157,11 +159,18 @@ constexpr int kWideN = 2048;
 // outputs of the LDS kernel up to this width use 8-column workgroups (HDCM_OPT_SKINNY_COLS8_MAX_N)
 inline bool cols8(int N) { return N <= hdcm_option_value(HDCM_OPT_SKINNY_COLS8_MAX_N); }
 
+// Second tiles (without LN): a launch of more column tiles than fit on the GPU at once would
+// run its last tiles as a second round of workgroups, each paying the full load latency again.
+// Instead the grid is one round and workgroup i < second_tiles also computes tile gridDim.x + i: its
+// waves load that tile's B fragments straight from W into registers (16 rows x 64 bytes per
+// instruction) together with the slab loads, reuse the A fragments, and sum the partial tiles
+// through their own slab regions (`second_tiles` of them).  Same K split and summation order, so the values are those
+// of a workgroup of its own.
 template <int STEPS, bool BIAS, bool RES, bool LN = false, int NCOL = 16>
 __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
     const bf16_t* __restrict__ A, int64_t a_rs, const bf16_t* __restrict__ W, int64_t w_rs,
     const bf16_t* __restrict__ bias, const bf16_t* __restrict__ res, int64_t r_rs,
-    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K, float eps = 0.f) {
+    bf16_t* __restrict__ out, int64_t o_rs, int M, int N, int K, float eps, int second_tiles) {
   static_assert(NCOL == 16 || NCOL == 8, "columns per workgroup");
   constexpr int PITCH = STEPS * 32 + 8;  // slab row pitch (elements): +16 bytes staggers the banks
   constexpr int NLD = (NCOL * 4 * STEPS + kWave - 1) / kWave;  // 16-byte weight loads per lane
@@ -178,12 +187,29 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   // the K step a slot s < STEPS of this wave reads: its own, or (past its range) one inside the row
   auto step_of = [&](int s) { return min(s0 + max(min(s, my - 1), 0), nsteps - 1); };
 
-  // the epilogue's bias and residual value, loaded now so the epilogue waits for nothing
+  // second tile (see above): uniform per workgroup
+  const bool two = !LN && (int)blockIdx.x < second_tiles;
+  const int n1 = ((int)gridDim.x + (int)blockIdx.x) * NCOL;
+  // the epilogue's bias and residual values, loaded now so the epilogue waits for nothing
   // (thread tid < 16*NCOL: row tid / NCOL, column tid % NCOL)
-  float pre = 0.f;
+  float pre = 0.f, pre1 = 0.f;
   if (tid < 16 * NCOL && tid / NCOL < M && n0 + tid % NCOL < N) {
     if (BIAS) pre += bf2f(bias[n0 + tid % NCOL]);
     if (RES) pre += bf2f(res[(int64_t)(tid / NCOL) * r_rs + n0 + tid % NCOL]);
+  }
+  if (two && tid < 16 * NCOL && tid / NCOL < M && n1 + tid % NCOL < N) {
+    if (BIAS) pre1 += bf2f(bias[n1 + tid % NCOL]);
+    if (RES) pre1 += bf2f(res[(int64_t)(tid / NCOL) * r_rs + n1 + tid % NCOL]);
+  }
+  // the second tile's B fragments, issued first (the slab and A loads after them are then
+  // waited for with the same counts on both paths): lane (l16, g) takes row n1 + l16 % NCOL
+  Frag<bf16_t> b1[LN ? 1 : STEPS];
+  if constexpr (!LN) {
+    if (two) {
+      const bf16_t* w1p = W + (int64_t)min(n1 + l16 % NCOL, N - 1) * w_rs + 8 * g;
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) b1[s].v = *reinterpret_cast<const bf16x8_t*>(w1p + 32 * step_of(s));
+    }
   }
   // piece idx of the wave's NCOL rows x STEPS steps x 4 sixteen-byte quarters; indices past
   // them (NCOL*STEPS not a multiple of 16) re-read the last piece and are not staged
@@ -228,6 +254,22 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
   // D layout: lane holds D[4 g + r][l16]
 #pragma unroll
   for (int r = 0; r < 4; ++r) part[w][4 * g + r][l16] = acc[r];
+  // the second tile's partial goes to the start of this wave's own slab, whose reads are done
+  // (a wave's LDS accesses complete in order; the empty asm keeps the compiler from moving the
+  // float stores above the bf16 reads of the same bytes)
+  static_assert(NCOL * PITCH * sizeof(bf16_t) >= 16 * 17 * sizeof(float), "slab holds a partial tile");
+  float* part1 = reinterpret_cast<float*>(sl);
+  if constexpr (!LN) {
+    if (two) {
+      asm volatile("" ::: "memory");
+      f32x4_t acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s)
+        if (s < my) acc1 = mma(fa[s], b1[s], acc1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part1[(4 * g + r) * 17 + l16] = acc1[r];
+    }
+  }
   __syncthreads();
   if (tid < 16 * NCOL) {
     const int m = tid / NCOL, nn = tid % NCOL, n = n0 + nn;
@@ -238,27 +280,66 @@ __global__ __launch_bounds__(kLdsThreads) void skinny_lds_kernel(
       if constexpr (LN) v = ln_apply<kLdsWaves>(lnst, m, nn, K, eps, v);
       out[(int64_t)m * o_rs + n] = f2bf(v + pre);
     }
+    if (two) {
+      float v1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < kLdsWaves; ++k) v1 += reinterpret_cast<const float*>(slab[k])[m * 17 + nn];
+      if (m < M && n1 + nn < N) out[(int64_t)m * o_rs + n1 + nn] = f2bf(v1 + pre1);
+    }
   }
+}
+
+// Workgroups of skinny_lds_kernel<STEPS, BIAS, RES, false, NCOL> resident at once on the current
+// device (occupancy per CU x CUs), found once per device; 0 if the runtime cannot tell.
+template <int STEPS, bool BIAS, bool RES, int NCOL>
+int lds_resident() {
+  static std::atomic<int> cache[16];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, skinny_lds_kernel<STEPS, BIAS, RES, false, NCOL>,
+                                                     kLdsThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      per_cu = cus = 0;
+    v = per_cu > 0 && cus > 0 ? per_cu * cus : -1;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v > 0 ? v : 0;
+}
+
+// One round of workgroups with second tiles when the tiles exceed one round by at most a
+// round (HDCM_OPT_SKINNY_FOLD_TAIL); otherwise a workgroup per tile.
+template <int STEPS, bool BIAS, bool RES, int NCOL>
+void launch_lds_one(const bf16_t* a, int64_t a_rs, const bf16_t* wt, int64_t w_rs, const bf16_t* bs,
+                    const bf16_t* rs, int64_t r_rs, bf16_t* o, int64_t o_rs, int M, int N, int K, hipStream_t s) {
+  const int tiles = (N + NCOL - 1) / NCOL;
+  int grid = tiles, extra = 0;
+  if (hdcm_option_value(HDCM_OPT_SKINNY_FOLD_TAIL)) {
+    const int res_wgs = lds_resident<STEPS, BIAS, RES, NCOL>();
+    if (res_wgs > 0 && tiles > res_wgs && tiles <= 2 * res_wgs) {
+      grid = res_wgs;
+      extra = tiles - res_wgs;
+    }
+  }
+  HDCM_LAUNCH((skinny_lds_kernel<STEPS, BIAS, RES, false, NCOL>), dim3((unsigned)grid), dim3(kLdsThreads), 0, s, a,
+              a_rs, wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f, extra);
 }
 
 template <int STEPS, int NCOL>
 void launch_lds_cols(const void* A, int64_t a_rs, const void* W, int64_t w_rs, const void* bias, const void* res,
                      int64_t r_rs, void* out, int64_t o_rs, int M, int N, int K, hipStream_t s) {
-  const dim3 grid((unsigned)((N + NCOL - 1) / NCOL));
   const bf16_t *a = (const bf16_t*)A, *wt = (const bf16_t*)W, *bs = (const bf16_t*)bias, *rs = (const bf16_t*)res;
   bf16_t* o = (bf16_t*)out;
   if (bias && res)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, true, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
-                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    launch_lds_one<STEPS, true, true, NCOL>(a, a_rs, wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, s);
   else if (bias)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, true, false, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
-                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    launch_lds_one<STEPS, true, false, NCOL>(a, a_rs, wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, s);
   else if (res)
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs, wt,
-                w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    launch_lds_one<STEPS, false, true, NCOL>(a, a_rs, wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, s);
   else
-    HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, false, false, NCOL>), grid, dim3(kLdsThreads), 0, s, a, a_rs,
-                wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, 0.f);
+    launch_lds_one<STEPS, false, false, NCOL>(a, a_rs, wt, w_rs, bs, rs, r_rs, o, o_rs, M, N, K, s);
 }
 
 template <int STEPS>
@@ -300,10 +381,10 @@ void launch_ln(const bf16_t* c, int64_t c_rs, const bf16_t* W, int64_t w_rs, con
     if (cols8(N))
       HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true, 8>), dim3((unsigned)((N + 7) / 8)),
                   dim3(kLdsThreads), 0, s, c, c_rs, W, w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K,
-                  eps);
+                  eps, 0);
     else
       HDCM_LAUNCH((skinny_lds_kernel<STEPS, false, true, true>), grid, dim3(kLdsThreads), 0, s, c, c_rs, W,
-                  w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps);
+                  w_rs, (const bf16_t*)nullptr, res, r_rs, out, o_rs, M, N, K, eps, 0);
   }
   else
     HDCM_LAUNCH((skinny_gemm_kernel<STEPS, false, true, true>), grid, dim3(kThreads), 0, s, c, c_rs, W,

@@ -78,15 +78,21 @@ int hdcm_timed_launch_count(void);
  *    outputs (hdcm_skinny_gemm_fwd, hdcm_rowln_gemm_fwd at <= 16 rows) of 2048 up to this
  *    many columns run 8 output columns per workgroup instead of 16 (0 switches it off).
  *    Results do not depend on it.
+ *  HDCM_OPT_SKINNY_FOLD_TAIL (env HDCM_SKINNY_FOLD_TAIL, default 1): skinny GEMM outputs
+ *    (N >= 2048, no folded LayerNorm) with more 16- or 8-column tiles than workgroups fit on
+ *    the GPU at once, but at most twice as many, run one round of workgroups, the first ones
+ *    taking a second tile, instead of a second round (0 switches it off).  Results do not
+ *    depend on it.
  * hdcm_set_option returns HDCM_EINVAL for an unknown option or a value out of range
- * (0 .. 2^20, the last one 0 .. 2^30); hdcm_get_option returns the current value (0 for an
+ * (0 .. 2^20; SKINNY_COLS8_MAX_N 0 .. 2^30; SKINNY_FOLD_TAIL 0 .. 1); hdcm_get_option returns the current value (0 for an
  * unknown one).
  * No counterpart in the reference (its launch table, model.py:12-19, is fixed).
  */
 typedef enum {
   HDCM_OPT_SSM_SPIN_ROUNDS = 1,
   HDCM_OPT_SLOT_SEG_TILES = 2,
-  HDCM_OPT_SKINNY_COLS8_MAX_N = 3
+  HDCM_OPT_SKINNY_COLS8_MAX_N = 3,
+  HDCM_OPT_SKINNY_FOLD_TAIL = 4
 } hdcm_option;
 int hdcm_set_option(int option, int value);
 int hdcm_get_option(int option);

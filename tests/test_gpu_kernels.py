@@ -424,6 +424,38 @@ def test_skinny_columns_per_workgroup(dev, M, N, K, bias, res, ln):
     assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
 
 
+@pytest.mark.parametrize("M,N,K,bias,res,cols8", [
+    (16, 8576, 2048, True, False, False),   # the d_model 2048 decode in_proj: 536 column tiles
+    (16, 8208, 2048, False, True, False),   # one tile past a round of 512 workgroups
+    (5, 16384, 1024, True, True, False),    # exactly two rounds' worth
+    (16, 8576, 2048, True, False, True),    # 8-column tiles
+    (16, 8584, 2048, True, False, False),   # the last tile half full
+])
+def test_skinny_fold_tail(dev, M, N, K, bias, res, cols8):
+    """The tiles past one round of resident workgroups, taken as second tiles by the first
+    workgroups, give the same bits as a second round of workgroups."""
+    _say("skinny fold tail", M, N, K, bias, res, cols8)
+    g = torch.Generator().manual_seed(N + K)
+    A = (1.5 * torch.randn(M, K, generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    W = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(dev)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16).to(dev) if bias else None
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev) if res else None
+    outs = []
+    with _ops.option("skinny_cols8_max_n", (1 << 30) if cols8 else 0):
+        for fold in (0, 1):
+            with _ops.option("skinny_fold_tail", fold):
+                outs.append(_ops.skinny_linear(A, W, b, r))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = A.float().cpu() @ W.float().cpu().t()
+    if bias:
+        ref = ref + b.float().cpu()
+    if res:
+        ref = ref + r.float().cpu()
+    err = (outs[1].float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
+
+
 def test_skinny_gemm_in_place_residual(dev):
     """out may be the residual buffer itself."""
     g = torch.Generator().manual_seed(3)
