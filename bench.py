@@ -451,10 +451,15 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
     # bytes one step must move: every parameter once (the tied head counted once) plus the
-    # carried states (slot: read S_prev, read+write S_intra; SSM: read+write h; conv history)
+    # carried states: slot, one fp32 state read and one written per token (S_intra between the
+    # tokens of a chunk, S_prev at its first and last), plus S_prev read again at a chunk's
+    # last token (1/C of the steps); SSM h read and written; the conv history's 3 rows read and
+    # written (shifted)
     param_bytes = sum(p.numel() * p.element_size() for p in lm.parameters())
     st = states[0]
-    state_bytes = len(states) * (3 * st.S_prev.numel() * 4 + 2 * st.h.numel() * 4 + 2 * st.conv.numel() * 2)
+    C = lm.backbone.layers[0].chunk_size
+    state_bytes = len(states) * ((2 + 1 / C) * st.S_prev.numel() * 4 + 2 * st.h.numel() * 4
+                                 + 2 * st.conv.numel() * 2)
     ms = sec / steps * 1e3
     gbs = (param_bytes + state_bytes) / (ms * 1e-3) / 1e9
     out = {

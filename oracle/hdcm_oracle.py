@@ -496,13 +496,18 @@ def model_forward(sd, x, cfg: BlockCfg, n_layers, semantics="intended", layers=N
 
 
 def lm_forward(sd, ids, cfg: BlockCfg, n_layers, semantics="intended", layers=None, n_prefill=None,
-               positions=None):
+               positions=None, return_hidden=False):
     """UniversalLM.forward, HdcMamba arm (train_fineweb.py:86-94): embedding, backbone,
     norm_f, tied lm_head.  ``n_prefill`` as in model_forward.  With ``positions`` (a list of
     token positions) the head runs on those positions only: logits [B, len(positions), V]
-    (the backbone still runs over the whole sequence)."""
+    (the backbone still runs over the whole sequence).  With ``return_hidden`` the result is
+    (logits, h), h [B, L, d_model] the head's input (norm_f's output) at every position."""
     x = F.embedding(ids, sd["embedding.weight"])
     x = model_forward(_sub(sd, "backbone."), x, cfg, n_layers, semantics, layers, n_prefill)
+    if return_hidden:
+        h = F.layer_norm(x, (cfg.d_model,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)
+        hp = h if positions is None else h[:, list(positions)]
+        return F.linear(hp, sd["embedding.weight"]), h
     if positions is not None:
         x = x[:, list(positions)]
     x = F.layer_norm(x, (cfg.d_model,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)

@@ -244,9 +244,10 @@ def test_empty_inputs(dev):
 @pytest.mark.parametrize("name", ["lm_c3", "lm_c4"])
 def test_lm_logits_against_oracle(dev, name):
     """The whole headline LM end to end in bf16 (12 layers d_model 768 at B=8 x 4096, and 24
-    layers d_model 1024 d_state 128 at B=1 x 32768; vocab 50304, default init): the logits
-    at 64 positions per sequence (the last 16 and 48 drawn at random) against the oracle's
-    LM forward (the whole backbone on the CPU, the head at those positions), normwise."""
+    layers d_model 1024 d_state 128 at B=1 x 32768; vocab 50304, default init) against the
+    oracle's LM forward (the whole backbone on the CPU): the head's input (norm_f's output) at
+    every position, and the logits at 64 positions per sequence (the last 16 and 48 drawn at
+    random), normwise."""
     cfg = WORKLOADS[name]
     print("lm end to end", name, flush=True)
     lm = make_lm(name, seed=5).to(torch.bfloat16)
@@ -254,13 +255,21 @@ def test_lm_logits_against_oracle(dev, name):
     L = ids.shape[1]
     g = torch.Generator().manual_seed(7)
     pos = sorted(set(torch.randint(0, L - 16, (48,), generator=g).tolist()) | set(range(L - 16, L)))
-    with torch.no_grad():
-        logits = lm.to(dev)(ids.to(dev))
+    seen = {}
+    hook = lm.lm_head.register_forward_pre_hook(lambda m, a: seen.__setitem__("h", a[0].float().cpu()))
+    try:
+        with torch.no_grad():
+            logits = lm.to(dev)(ids.to(dev))
+    finally:
+        hook.remove()
     got = logits[:, pos].float().cpu()
     del logits
     torch.cuda.empty_cache()
-    ref = oracle.lm_forward(_sd(lm), ids, oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"],
-                                                          cfg["chunk"]), cfg["n_layers"], positions=pos)
-    print("max rel", max_rel(got, ref), flush=True)
+    ref, ref_h = oracle.lm_forward(_sd(lm), ids, oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"],
+                                                                 cfg["chunk"]), cfg["n_layers"], positions=pos,
+                                   return_hidden=True)
+    print("hidden max rel", max_rel(seen["h"], ref_h), "logits max rel", max_rel(got, ref), flush=True)
+    assert seen["h"].shape == ref_h.shape
+    assert_close_normwise(seen["h"], ref_h, torch.bfloat16, f"{name} head input, every position")
     assert_close_normwise(got, ref, torch.bfloat16, f"{name} logits")
 

@@ -379,3 +379,33 @@ def test_attend_gradients_are_attend_passes(C):
     dk = oracle.attend_chunked(fl(v), fl(dy), fl(qf), gamma, C)[0].flip(1)
     for name, got, ref in (("dq", dq, qf.grad), ("dv", dv, v.grad), ("dk", dk, kf.grad)):
         torch.testing.assert_close(got, ref, atol=1e-4, rtol=1e-4, msg=name)
+
+
+# ----------------------------------------------------------------------------- LM wrapper
+def test_lm_forward_hidden_and_positions():
+    """lm_forward's head input (return_hidden) is norm_f over the blocks and norm_final composed
+    by hand, and the logits at chosen positions are the tied head applied to it there."""
+    cfg = oracle.BlockCfg(16, 4, 2, 4)
+    V, n_layers = 40, 2
+    sd = {}
+    for i in range(n_layers):
+        for k, v in oracle.init_block_params(cfg, generator_seed=20 + i).items():
+            sd[f"backbone.layers.{i}.{k}"] = v
+    g = _g(21)
+    sd["backbone.norm_final.weight"] = 1 + 0.1 * torch.randn(16, generator=g)
+    sd["backbone.norm_final.bias"] = 0.1 * torch.randn(16, generator=g)
+    sd["norm_f.weight"] = 1 + 0.1 * torch.randn(16, generator=g)
+    sd["norm_f.bias"] = 0.1 * torch.randn(16, generator=g)
+    sd["embedding.weight"] = torch.randn(V, 16, generator=g)
+    ids = torch.randint(0, V, (2, 10), generator=g)
+    pos = [0, 3, 9]
+    logits, h = oracle.lm_forward(sd, ids, cfg, n_layers, positions=pos, return_hidden=True)
+    x = F.embedding(ids, sd["embedding.weight"])
+    for i in range(n_layers):
+        x = oracle.block_forward({k[len(f"backbone.layers.{i}."):]: v for k, v in sd.items()
+                                  if k.startswith(f"backbone.layers.{i}.")}, x, cfg)
+    x = F.layer_norm(x, (16,), sd["backbone.norm_final.weight"], sd["backbone.norm_final.bias"], 1e-5)
+    want_h = F.layer_norm(x, (16,), sd["norm_f.weight"], sd["norm_f.bias"], 1e-5)
+    torch.testing.assert_close(h, want_h, atol=1e-6, rtol=1e-6)
+    torch.testing.assert_close(logits, F.linear(want_h[:, pos], sd["embedding.weight"]), atol=1e-5, rtol=1e-5)
+    assert torch.equal(logits, oracle.lm_forward(sd, ids, cfg, n_layers, positions=pos))
