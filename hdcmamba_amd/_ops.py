@@ -66,6 +66,9 @@ _PROTOS = {
                                     c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_float,
                                     c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                                     c_int, c_void_p]),
+    "hdcm_gnorm_gate_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                    c_float, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int,
+                                    c_void_p]),
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
     "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                      c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
@@ -482,6 +485,9 @@ def slot_phi_chain(projs, q_col, d_model, dprojs):
     return dprojs
 
 
+SLOT_MAX_HEAD_DIM = 128  # widest head of the fused slot + gate kernels
+
+
 def slot_workspace(projs, d_model, num_heads, chunk):
     B, L, _ = projs.shape
     nbytes = lib().hdcm_slot_workspace_bytes(B, L, d_model, num_heads, chunk, _dtype(projs))
@@ -558,6 +564,26 @@ def slot_gate(projs, q_col, gamma, gn_w, gn_b, gn_eps, ws, out, out_col, d_model
         out_col, S_final.data_ptr() if S_final is not None else None, sp, srs, B, L, d_model, num_heads, chunk,
         _dtype(projs), _stream(projs)))
     timer.end("slot_gate", ev)
+    return out
+
+
+def gnorm_gate(y1, y2, gate, gn_w, gn_b, gn_eps, num_heads, out, row_stats=None, stats_part=0):
+    """GroupNorm per (token, head) of y1 + y2' (y2' = y2 with each head's halves exchanged; y2
+    may be None) times sigmoid(gate), into ``out``; all [..., d_model] row views of one dtype.
+    ``row_stats`` as in slot_gate."""
+    _on_gpu(y1, gate, out)
+    dm = y1.shape[-1]
+    rows = y1.numel() // dm if dm else 0
+    gn_w = _same(gn_w, y1, "gn_w")
+    gn_b = _same(gn_b, y1, "gn_b")
+    sp, srs = _stats_arg(row_stats, stats_part, rows, num_heads)
+    ev = timer.begin("gnorm_gate")
+    _check("hdcm_gnorm_gate_fwd", lib().hdcm_gnorm_gate_fwd(
+        y1.data_ptr(), _rows2d(y1, "y1"), y2.data_ptr() if y2 is not None else None,
+        _rows2d(y2, "y2") if y2 is not None else 0, gate.data_ptr(), _rows2d(gate, "gate"), gn_w.data_ptr(),
+        gn_b.data_ptr(), float(gn_eps), out.data_ptr(), _rows2d(out, "out"), sp, srs, rows, dm, num_heads,
+        _dtype(y1), _stream(y1)))
+    timer.end("gnorm_gate", ev)
     return out
 
 

@@ -262,6 +262,13 @@ class HdcMamba9v3Block(nn.Module):
 
         gamma = self.gamma_buf.to(dtype)
         q_col = 3 * ds
+        if self.head_dim > _ops.SLOT_MAX_HEAD_DIM:
+            mode = "none"  # the scan first (run_ssm reads mode when called)
+            run_ssm()
+            self._wide_slot_gate(projs, combined, gamma, row_stats, state)
+            if normalize:
+                _ops.layer_norm(combined, eps=1e-5, out=combined)
+            return combined.view(B * L, ds + dm)
         ws = _ops.slot_workspace(projs, dm, H, C)
         if mode != "after_state":
             run_ssm()
@@ -278,6 +285,36 @@ class HdcMamba9v3Block(nn.Module):
         if normalize:
             _ops.layer_norm(combined, eps=1e-5, out=combined)
         return combined.view(B * L, ds + dm)
+
+    def _wide_slot_gate(self, projs, combined, gamma, row_stats, state):
+        """Slot memory + GroupNorm + gate for a head dim above the fused kernels' 128 (the
+        reference pads any head dim, model.py:245-246,286): a head of hd = 2 hb columns runs as two
+        sub-heads of hb through the plain slot pass (hdcm_slot_attend_fwd, the head's decay for
+        both).  The scores split over the two key blocks, phi(q).phi(k) = sum_b phi(q_b).phi(k_b),
+        so value block c of the output is attend(q_c, k_c, v_c) + attend(q_b, k_b, v_c), b != c: the
+        first pass gives the equal-block terms, the second, after the two value halves of every
+        head in projs are exchanged, the crossed ones (at the other half's columns); then the
+        GroupNorm over all hd values of their sum and the gate (hdcm_gnorm_gate_fwd).  projs'
+        value columns are left exchanged.  Forward only: hd a multiple of 32 up to 256, no state
+        hand-off."""
+        B, L, _ = projs.shape
+        dm, ds, H, C = self.d_model, self.d_state, self.num_heads, self.chunk_size
+        hd = dm // H
+        if hd % 32 or hd > 2 * _ops.SLOT_MAX_HEAD_DIM:
+            raise _ops.HdcmError(f"slot memory (head dim {hd})", -3)
+        if state is not None:
+            raise _ops.HdcmError(f"slot memory state hand-off (head dim {hd})", -3)
+        q_col = 3 * ds
+        g2 = gamma.repeat_interleave(2)
+        ws = _ops.slot_workspace(projs, dm, 2 * H, C)
+        y1 = torch.empty(B, L, dm, device=projs.device, dtype=projs.dtype)
+        y2 = torch.empty_like(y1)
+        _ops.slot_attend(projs, q_col, q_col + dm, q_col + 2 * dm, g2, dm, 2 * H, C, True, y1, 0, ws=ws)
+        v = projs[..., q_col + 2 * dm:q_col + 3 * dm].unflatten(-1, (H, 2, hd // 2))
+        v.copy_(v.flip(-2))
+        _ops.slot_attend(projs, q_col, q_col + dm, q_col + 2 * dm, g2, dm, 2 * H, C, True, y2, 0, ws=ws)
+        _ops.gnorm_gate(y1, y2, projs[..., q_col + 3 * dm:], self.group_norm.weight, self.group_norm.bias, 1e-5, H,
+                        combined[..., ds:], row_stats=row_stats, stats_part=_ops.ssm_stats_parts(ds))
 
     def _fused_out(self, x):
         """Whether out_proj runs as the GEMM with the LayerNorm folded in (bf16, no autograd).
@@ -356,6 +393,8 @@ class HdcMamba9v3Block(nn.Module):
         if self._fused_out(x):
             return self._fused_mixer_out(x, state)
         if self.differentiable_mixer and state is None and torch.is_grad_enabled():
+            if self.head_dim > _ops.SLOT_MAX_HEAD_DIM:
+                raise _ops.HdcmError(f"differentiable slot memory (head dim {self.head_dim})", -3)
             c = self._differentiable_mixer(x)
         else:
             c = self._mixer(x, state)

@@ -250,6 +250,24 @@ int hdcm_slot_attend_fwd(const void* base, int64_t row_stride, int64_t q_col, in
                          int64_t C, int dtype, void* stream);
 
 /*
+ * The per-token, per-head GroupNorm (eps, affine gn_w/gn_b over hd = dm/H values) and sigmoid
+ * gate of hdcm_slot_gate_fwd as a pass of its own, for heads wider than that pass holds
+ * (hd > 128): out = GN(y) * sigmoid(gate) on `rows` token rows, y = y1 + y2', y2' being y2
+ * with the two halves of every head exchanged (y2 may be NULL; with it hd must be even), so
+ * that a head of 2*hb columns can run its slot recurrence as two sub-heads of hb through
+ * hdcm_slot_attend_fwd (equal key and value blocks in y1, crossed ones in y2 after its value
+ * halves were exchanged).  row_stats (or NULL): per row r and head h the (sum, sum of squares)
+ * of the hd stored values at row_stats[2*(h*stats_part_stride + r)], as hdcm_slot_gate_fwd
+ * writes them.  hd <= 512.
+ * Replaces: the slot part of _fused_gnorm_gate_cat_kernel (hdcmamba/model.py:274-293, launch
+ * model.py:375-380), whose BLOCK_SIZE_D = max(64, next_pow2(hd)) covers any head dim.
+ */
+int hdcm_gnorm_gate_fwd(const void* y1, int64_t y1_row_stride, const void* y2, int64_t y2_row_stride,
+                        const void* gate, int64_t gate_row_stride, const void* gn_w, const void* gn_b, float gn_eps,
+                        void* out, int64_t out_row_stride, float* row_stats, int64_t stats_part_stride,
+                        int64_t rows, int64_t dm, int64_t H, int dtype, void* stream);
+
+/*
  * Gradient of the per-token, per-head GroupNorm (eps, affine gn_w/gn_b over hd = dm/H
  * values) and sigmoid gate of hdcm_slot_gate_fwd, on `rows` token rows: from y (the slot
  * recurrence's output before the GroupNorm), the gate values and dout, writes dy and dgate

@@ -166,6 +166,27 @@ def test_decode_step_validation():
     assert lib.hdcm_chunk_pos_advance(None, 64, None) == EINVAL
 
 
+def test_gnorm_gate_validation():
+    # hdcm_gnorm_gate_fwd(y1, y1_rs, y2, y2_rs, gate, g_rs, gn_w, gn_b, eps, out, o_rs, row_stats, sps, rows,
+    #                     dm, H, dtype, stream)
+    f = _ops.lib().hdcm_gnorm_gate_fwd
+    base = [P16, 512, P16, 512, P16, 2048, P16, P16, 1e-5, P16, 640, None, 0, 4, 512, 2, 1, None]
+    a = list(base); a[16] = 2  # unknown dtype
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[0] = None
+    assert f(*a) == EINVAL
+    a = list(base); a[15] = 3  # d_model not a multiple of the heads
+    assert f(*a) == EINVAL
+    a = list(base); a[14] = 1024; a[15] = 1; a[1] = a[3] = a[5] = a[10] = 1024  # head dim 1024
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[14] = 510; a[15] = 2  # odd head dim with a second part
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[11] = P16; a[12] = 3  # statistics part stride below the row count
+    assert f(*a) == EINVAL
+    a = list(base); a[13] = 0
+    assert f(*a) == OK
+
+
 def test_skinny_gemm_validation():
     # hdcm_skinny_gemm_fwd(A, a_rs, W, w_rs, bias, res, res_rs, out, o_rs, M, N, K, dtype, stream)
     f = _ops.lib().hdcm_skinny_gemm_fwd

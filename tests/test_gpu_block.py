@@ -89,6 +89,31 @@ def test_block_general_head_dims_and_chunks(dev, dtype, dm, H, C, L):
     assert_close(y, ref, dtype, f"dm={dm} H={H} C={C}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dm,H,C,L", [(512, 2, 64, 200), (640, 4, 48, 150)])
+def test_block_wide_heads(dev, dtype, dm, H, C, L):
+    """Head dims above 128 (256, and 160 with chunk 48): each head as two sub-heads of the plain
+    slot pass plus the crossed key/value-block terms, then the GroupNorm over the whole head,
+    through the whole block (padding, the out_proj fold in bf16); prefill state hand-off and the
+    differentiable mixer are not built for them and raise."""
+    print("block wide heads", dtype, dm, H, C, L, flush=True)
+    from hdcmamba_amd import HdcMamba9v3Block
+    from cfgs import reinit_block_
+
+    torch.manual_seed(dm + H)
+    blk = reinit_block_(HdcMamba9v3Block(dm, 64, H, C), seed=dm + H, decays_uniform=True).eval().to(dtype)
+    assert blk.head_dim > 128
+    x = torch.randn(2, L, dm, generator=torch.Generator().manual_seed(L)).to(dtype)
+    ref = oracle.block_forward(_sd(blk), x, oracle_cfg(blk))
+    blk = blk.to(dev)
+    with torch.no_grad():
+        y, _ = blk(x.to(dev))
+    print("max rel", max_rel(y, ref), flush=True)
+    assert_close(y, ref, dtype, f"dm={dm} H={H} C={C}")
+    with torch.no_grad(), pytest.raises(RuntimeError):
+        blk.prefill(x.to(dev))
+
+
 def test_model_and_lm_small(dev):
     """2-layer LM (d_model 768, heads 12) at B=2, L=512 through embedding, blocks, norms, tied head."""
     print("lm small", flush=True)

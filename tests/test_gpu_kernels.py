@@ -456,6 +456,35 @@ def test_skinny_fold_tail(dev, M, N, K, bias, res, cols8):
     assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hd,H,two", [(256, 4, True), (160, 3, True), (96, 2, False)])
+def test_gnorm_gate_pass(dev, dtype, hd, H, two):
+    """The GroupNorm + gate pass of wide heads against oracle.gnorm_gate on y1 + y2' (y2 with
+    each head's halves exchanged), with its row statistics against the stored values."""
+    _say("gnorm gate pass", dtype, hd, H, two)
+    g = torch.Generator().manual_seed(hd + H)
+    rows, dm = 300, hd * H
+    y1 = (torch.randn(rows, dm, generator=g) + 0.3).to(dtype)
+    y2 = torch.randn(rows, dm, generator=g).to(dtype) if two else None
+    gate = torch.randn(rows, 2 * dm, generator=g).to(dtype)[:, dm // 2:dm // 2 + dm]  # a strided view
+    gn_w = (1 + 0.2 * torch.randn(dm, generator=g)).to(dtype)
+    gn_b = (0.1 * torch.randn(dm, generator=g)).to(dtype)
+    y = y1.float()
+    if two:
+        y = y + y2.float().view(rows, H, 2, hd // 2).flip(2).reshape(rows, dm)
+    ref = oracle.gnorm_gate(y.view(1, rows, H, hd), gate.float().view(1, rows, dm), gn_w, gn_b, H).view(rows, dm)
+    out = torch.zeros(rows, dm + 8, dtype=dtype, device=dev)[:, 8:]
+    stats = torch.zeros(H + 1, rows, 2, dtype=torch.float32, device=dev)
+    _ops.gnorm_gate(y1.to(dev), y2.to(dev) if two else None, gate.to(dev), gn_w.to(dev), gn_b.to(dev), 1e-5, H,
+                    out, row_stats=stats, stats_part=1)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, dtype, "gnorm gate")
+    o = out.float().cpu().view(rows, H, hd)
+    torch.testing.assert_close(stats[1:].cpu(), torch.stack([o.sum(-1), (o * o).sum(-1)], -1).transpose(0, 1),
+                               rtol=1e-5, atol=1e-4)
+    assert (stats[0] == 0).all()
+
+
 def test_skinny_gemm_in_place_residual(dev):
     """out may be the residual buffer itself."""
     g = torch.Generator().manual_seed(3)
