@@ -571,16 +571,21 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   // the buffer path with the agent-scope cache policy (coalesced, and never a stale L2 line;
   // each 8-byte half carries its own tag, so a read torn between two stores shows a stale
   // half and is read again)
-  auto read_window = [&](int j0, uint4 (&q)[CPW]) {
+  // (lanes with `again` false keep what they hold: after the first round only the tiles some
+  // wave still missed are read again)
+  auto read_window = [&](int j0, uint4 (&q)[CPW], bool again) {
     const int j = j0 + lane;
 #pragma unroll
     for (int k = 0; k < CPW; ++k) {
       const int c = w * CPW + k;
-      q[k] = make_uint4(0u, 0u, 0u, 0u);
-      if (j < tile && c < nch)
-        q[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             wrsrc, (int)(((seq * kScanCh + c) * ntiles + j) * 16), 0,
-                                             kCachePolicySC1));
+      if (j < tile && c < nch) {
+        if (again)
+          q[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               wrsrc, (int)(((seq * kScanCh + c) * ntiles + j) * 16), 0,
+                                               kCachePolicySC1));
+      } else {
+        q[k] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
   for (int j0 = 0; j0 < tile; j0 += kWave) {
@@ -588,8 +593,9 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     const bool act = j < tile;
     uint4 q[CPW];
     float va[CPW], vh[CPW];
+    unsigned long long all = ~0ull;  // tiles of the window to read: all of them, then the missed ones
     for (int round = 0;; ++round) {
-      read_window(j0, q);
+      read_window(j0, q, (all >> lane) & 1ull);
       bool ok = true;
 #pragma unroll
       for (int k = 0; k < CPW; ++k) {
@@ -610,7 +616,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
         s_missing[w][1] = (unsigned)(miss >> 32);
       }
       __syncthreads();
-      unsigned long long all = 0;
+      all = 0;
 #pragma unroll
       for (int k = 0; k < kScanWaves; ++k)
         all |= (unsigned long long)s_missing[k][0] | ((unsigned long long)s_missing[k][1] << 32);
