@@ -623,7 +623,7 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
       __syncthreads();
       if (all == 0) break;
       if (round < spin_rounds) {
-        __builtin_amdgcn_s_sleep(4);
+        __builtin_amdgcn_s_sleep(1);
         continue;
       }
       // still missing after the polling budget: compute those tiles' totals here, publish
