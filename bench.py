@@ -428,8 +428,9 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
     steps = args.steps if args.steps != 10 else 128
     warm = max(args.warmup, 2)
     lm = make_lm("lm_c5").to(torch.bfloat16).to(dev)
-    from hdcmamba_amd import set_fused_out_proj
+    from hdcmamba_amd import _ops, set_fused_out_proj, set_fused_step_front
     set_fused_out_proj(lm, args.fused_out_proj == "on")
+    set_fused_step_front(lm, args.fused_step_front == "on")
     ids = lm_input("lm_c5", B=B, L=L + warm + steps + 1).to(dev)
     with torch.no_grad():
         lm.prefill(ids[:, :256])  # warm the prefill kernels and GEMM handles
@@ -470,11 +471,12 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
         "config": {"workload": "48-layer d_model=2048 HdcMamba LM, prefill B=16 L=8192 then single-token decode",
                    "d_model": 2048, "d_state": 128, "num_heads": 32, "chunk": 64, "layers": 48, "vocab": 50304,
                    "global_batch": B, "prefill_len": L, "graph": not args.eager,
-                   "fused_out_proj": args.fused_out_proj == "on"},
+                   "fused_out_proj": args.fused_out_proj == "on", "fused_step_front": args.fused_step_front == "on"},
         "roofline": {"kernel": "whole decode step", "bound": "hbm", "achieved": round(gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": param_bytes + state_bytes},
         "prefill_tokens_per_s": round(B * L / t_prefill, 1),
+        "step_front_timeouts": _ops.step_timeouts(dev) if args.fused_step_front == "on" else None,
         "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)
@@ -551,6 +553,9 @@ def main():
     ap.add_argument("--fused-out-proj", default="on", choices=["on", "off"],
                     help="LM workloads: the LayerNorm of `combined`, out_proj and the residual add as one "
                          "GEMM with the LayerNorm in its epilogue (on) or a row LayerNorm kernel and addmm (off)")
+    ap.add_argument("--fused-step-front", default="on", choices=["on", "off"],
+                    help="lm_c5_decode: each block's LayerNorm + conv and in_proj of the token as one launch "
+                         "(on) or as two kernels (off)")
     ap.add_argument("--cpu-baseline", default="on", choices=["on", "off"])
     ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU-oracle forwards after one warm-up")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),

@@ -10,6 +10,7 @@ from .model import (
     fused_norm_conv1d_trainable,
     set_differentiable_mixer,
     set_fused_out_proj,
+    set_fused_step_front,
 )
 from .lm import DecodeGraph, ForwardGraph, HdcMambaLM
 
@@ -24,4 +25,5 @@ __all__ = [
     "ForwardGraph",
     "set_differentiable_mixer",
     "set_fused_out_proj",
+    "set_fused_step_front",
 ]

@@ -72,6 +72,11 @@ _PROTOS = {
     "hdcm_chunk_pos_advance": (c_int, [c_void_p, c_int64, c_void_p]),
     "hdcm_skinny_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                      c_void_p, c_int64, c_int64, c_int64, c_int64, c_int, c_void_p]),
+    "hdcm_step_workspace_bytes": (c_size_t, []),
+    "hdcm_norm_conv_in_proj_step_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                                c_void_p, c_float, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                                                c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_size_t,
+                                                c_int, c_void_p]),
     "hdcm_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64,
                               c_int64, c_int, c_void_p]),
     "hdcm_rowln_gemm_fwd": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
@@ -271,7 +276,8 @@ class _Timer:
 timer = _Timer()
 
 # launch options of the library (hdcm_set_option)
-OPTIONS = {"ssm_spin_rounds": 1, "slot_seg_tiles": 2, "skinny_cols8_max_n": 3, "skinny_fold_tail": 4}
+OPTIONS = {"ssm_spin_rounds": 1, "slot_seg_tiles": 2, "skinny_cols8_max_n": 3, "skinny_fold_tail": 4,
+           "step_spin_rounds": 5}
 
 
 class option:
@@ -281,7 +287,8 @@ class option:
     slot_seg_tiles = row tiles per slot segment (0 = automatic); skinny_cols8_max_n = widest
     skinny-GEMM output run with 8 columns per workgroup (0 = never); skinny_fold_tail = 1 runs
     the skinny GEMM's tiles past one round of resident workgroups as second tiles of the first
-    workgroups (0 = a second round).  Launches read the value
+    workgroups (0 = a second round); step_spin_rounds = polling rounds of the fused decode front's
+    GEMM workgroups for the conv rows before they count a timeout.  Launches read the value
     current when they are issued (a recorded graph keeps the value of its capture)."""
 
     def __init__(self, name, value):
@@ -676,6 +683,74 @@ def norm_conv_step(x, ln_w, ln_b, conv_w, conv_b, eps, hist, out=None):
         hist.data_ptr(), out.data_ptr(), out.stride(0), B, D, float(eps), _dtype(x), _stream(x)))
     timer.end("norm_conv_step", ev)
     return out
+
+
+_step_ws = {}  # device index -> the fused decode front's flag workspace
+
+
+def step_workspace(device):
+    """The fused decode front's workspace (call tag, arrivals, timeouts, row flags) of
+    `device`: zero-filled once, then kept (the kernel keeps it consistent from call to call).
+    One per device, shared by every stream: calls that overlap in time on one device race
+    (a decode step, eager or replayed, runs on one stream at a time)."""
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _step_ws.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("decode step: the fused front's workspace must exist before graph capture; run "
+                               "one step outside capture first")
+        nbytes = int(lib().hdcm_step_workspace_bytes())
+        ws = torch.zeros((nbytes + 255) // 256 * 256, dtype=torch.uint8, device=device)
+        _step_ws[key] = ws
+    return ws
+
+
+def step_timeouts(device) -> int:
+    """Waits of the fused decode front that gave up (the word at byte 128 of the workspace) on `device`;
+    0 unless the GPU was shared with work that held back the conv rows."""
+    ws = step_workspace(device)
+    return int(ws[128:132].view(torch.int32).item())
+
+
+def norm_conv_in_proj_step_ok(x, weight) -> bool:
+    """Whether the fused decode front (hdcm_norm_conv_in_proj_step_fwd) takes x [B,D] and
+    in_proj's weight [N,D]: bf16, 1 <= B <= 16, D % 32 == 0, D <= 2048."""
+    B, D = x.shape
+    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and 1 <= B <= SKINNY_MAX_ROWS
+            and D % 32 == 0 and D <= 2048 and weight.shape[-1] == D)
+
+
+def norm_conv_in_proj_step(x, ln_w, ln_b, conv_w, conv_b, eps, hist, weight, bias, u=None, out=None):
+    """norm_conv_step followed by skinny_linear(u, weight, bias) in one launch (the same values
+    bit for bit): x [B,D] -> (u [B,D], out [B,N]); hist [B,3,D] is shifted in place."""
+    _on_gpu(x, hist, weight)
+    B, D = x.shape
+    N = weight.shape[0]
+    ln_w = _same(ln_w, x, "ln_w")
+    ln_b = _same(ln_b, x, "ln_b")
+    conv_b = _same(conv_b, x, "conv_b")
+    conv_w = _same(conv_w.reshape(D, 4), x, "conv_w")
+    if hist.dtype != x.dtype or not hist.is_contiguous() or tuple(hist.shape) != (B, 3, D):
+        raise RuntimeError("norm_conv_in_proj_step: hist must be a contiguous [B,3,D] tensor of x's dtype")
+    if x.stride(1) != 1 or x.stride(0) % 8:
+        x = x.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    if bias is not None:
+        bias = _same(bias, x, "bias")
+    if u is None:
+        u = torch.empty(B, D, device=x.device, dtype=x.dtype)
+    if out is None:
+        out = torch.empty(B, N, device=x.device, dtype=x.dtype)
+    ws = step_workspace(x.device)
+    ev = timer.begin("norm_conv_in_proj_step")
+    _check("hdcm_norm_conv_in_proj_step_fwd", lib().hdcm_norm_conv_in_proj_step_fwd(
+        x.data_ptr(), x.stride(0), ln_w.data_ptr(), ln_b.data_ptr(), conv_w.data_ptr(), conv_b.data_ptr(),
+        hist.data_ptr(), float(eps), u.data_ptr(), u.stride(0), w.data_ptr(), w.stride(0),
+        bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0), B, D, N, ws.data_ptr(),
+        ws.numel(), _dtype(x), _stream(x)))
+    timer.end("norm_conv_in_proj_step", ev)
+    return u, out
 
 
 def mixer_step(projs, A_log, d_state, q_col, gamma, gn_w, gn_b, gn_eps, h, S_prev, S_intra, pos, chunk,

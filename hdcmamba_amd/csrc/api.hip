@@ -23,6 +23,7 @@ constexpr OptionInfo kOptions[] = {
     {"HDCM_SLOT_SEG_TILES", 0, 0, 1 << 20},     // HDCM_OPT_SLOT_SEG_TILES (0: automatic)
     {"HDCM_SKINNY_COLS8_MAX_N", 4096, 0, 1 << 30},  // HDCM_OPT_SKINNY_COLS8_MAX_N
     {"HDCM_SKINNY_FOLD_TAIL", 1, 0, 1},            // HDCM_OPT_SKINNY_FOLD_TAIL
+    {"HDCM_STEP_SPIN_ROUNDS", 65536, 0, 1 << 24},  // HDCM_OPT_STEP_SPIN_ROUNDS
 };
 constexpr int kNumOptions = sizeof(kOptions) / sizeof(kOptions[0]);
 

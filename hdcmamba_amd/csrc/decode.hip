@@ -180,6 +180,15 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
   const int64_t sbase = (((int64_t)b * H + h) * HD) * HD + 4 * cgi;
   // chunk offset: from device memory when the step runs inside a captured graph
   const int c = c_dev != nullptr ? __builtin_amdgcn_readfirstlane(*c_dev) : c_arg;
+  // This token's q, k, v (needed first, for the LDS vectors), its gate and the GroupNorm
+  // affine go out ahead of the states and are converted only after the state loads are
+  // issued, so the wait for them overlaps the states' round trip.  Branch-free at a clamped
+  // column (threads past HD load column HD-1 and do not use it).
+  const T* q = row + q_col + h * HD;
+  const int hc = min(tid, HD - 1);
+  const T q_raw = q[hc], k_raw = q[dm + hc], v_raw = q[2 * dm + hc];
+  const T gate_raw = row[q_col + 3 * dm + h * HD + hc], gnw_raw = gn_w[h * HD + hc], gnb_raw = gn_b[h * HD + hc];
+  const T gamma_raw = gamma[h];
   // The state the token builds on: the previous token's S_eff kept in S_intra, loaded while
   // the offset is still in flight (right for every token but a chunk's first), or S_prev at a
   // chunk's first token; S_prev again at a chunk's last token, where it is folded into the
@@ -199,22 +208,13 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
       else if (last) sp[k] = *reinterpret_cast<const float4*>(S_prev + sbase + (int64_t)i * HD);
     }
   }
-  // this thread's gate and GroupNorm parameters, loaded with the states (used last)
-  T gate_raw = T(), gnw_raw = T(), gnb_raw = T();
-  if (tid < HD) {
-    const int col = h * HD + tid;
-    gate_raw = row[q_col + 3 * dm + col];
-    gnw_raw = gn_w[col];
-    gnb_raw = gn_b[col];
-  }
-  const float g = to_f<T>(gamma[h]);
+  const float g = to_f<T>(gamma_raw);
   const float lg2 = log2f(g);
-  const T* q = row + q_col + h * HD;
   if (tid < HD) {
     // phi(q), phi(k) rounded to the activation dtype as in the chunked kernels' operands
-    sq[tid] = rnd<T>(phi_f(to_f<T>(q[tid])));
-    sk[tid] = rnd<T>(phi_f(to_f<T>(q[dm + tid])));
-    sv[tid] = to_f<T>(q[2 * dm + tid]);
+    sq[tid] = rnd<T>(phi_f(to_f<T>(q_raw)));
+    sk[tid] = rnd<T>(phi_f(to_f<T>(k_raw)));
+    sv[tid] = to_f<T>(v_raw);
   }
   __syncthreads();
 

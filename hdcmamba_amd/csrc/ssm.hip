@@ -21,10 +21,12 @@
 // agent-scope atomic words {value, tag} that bypass the non-coherent per-XCD L2s, one word
 // for A and one for H, so a reader needs no fence: a word is valid when its tag is this
 // call's.  The tag is an epoch kept in the workspace header, read by every workgroup at its
-// start; each workgroup then counts itself in the header (an atomic whose latency hides
-// behind its loads), and the last to arrive advances the epoch when it ends (every workgroup
-// has read the tag by then, and nothing reads the header again in this call), so the
-// workspace never needs clearing
+// start; each workgroup then counts itself in one of eight counters of the header (an atomic
+// whose latency hides behind its loads; the workgroup that completes a counter counts it in a
+// ninth), and the last to arrive advances the epoch when it ends (every workgroup has read the
+// tag by then, and nothing reads the header again in this call), so the workspace never needs
+// clearing.  The tag and the counters sit on 128-byte lines of their own: one counter on the
+// tag's line took every workgroup's arrival in turn, ~1 us of the scan at 256 workgroups
 // (it must be zero before its first use).  A workgroup that finds an earlier total missing
 // polls for a bounded number of rounds, then computes that tile's total itself with the
 // same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
@@ -231,7 +233,11 @@ inline int64_t ssm_tiles(int64_t L) { return (L + kTile - 1) / kTile; }
 constexpr int kScanThreads = 512;
 constexpr int kScanCh = 32;  // channels per workgroup
 constexpr int kScanWaves = kScanThreads / kWave;
-constexpr int kHeaderBytes = 256;  // workspace header: epoch, finished-workgroup count
+// workspace header: the epoch (word 0), eight arrival counters and the count of completed
+// counters, each on a 128-byte line of its own (words 32, 64, ..., 288)
+constexpr int kHeaderBytes = 2048;
+constexpr int kHdrLine = 32;     // u32 words per 128-byte line
+constexpr int kArrivalGroups = 8;
 constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3: raw 32-bit dwords
 constexpr int kCachePolicySC1 = 16;       // buffer load cache policy: agent-scope coherent (sc1)
 
@@ -260,7 +266,7 @@ __device__ __forceinline__ void scan_unpack(ScanRaw<T> v, float (&o)[ScanShape<T
   unpack16<T>(v, o);
 }
 
-// Workspace layout: header (epoch, finished-workgroup count), then the tile totals: per
+// Workspace layout: header (epoch, arrival counters), then the tile totals: per
 // sequence (batch row x channel block), channel and tile one 16-byte (A, H) pair of tagged
 // words.
 struct ScanWorkspace {
@@ -530,7 +536,9 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
   if (tid == 0) {
     unsigned zero;
     __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(tag));
-    arrived = __hip_atomic_fetch_add(hdr + 1 + zero, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    arrived = __hip_atomic_fetch_add(hdr + kHdrLine * (1 + lin % kArrivalGroups) + zero, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
   }
 
   float negA[E];
@@ -701,10 +709,21 @@ __global__ __launch_bounds__(kScanThreads) void ssm_scan_kernel(
     }
   }
 
-  // ---- the last workgroup to arrive advances the epoch and resets the count for the next call
-  if (tid == 0 && arrived == gridDim.x * gridDim.y * gridDim.z - 1) {
-    __hip_atomic_store(hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ---- the workgroup that completes its counter counts it in the last one; the one that
+  // completes that advances the epoch and clears the counters for the next call
+  if (tid == 0) {
+    const unsigned G = gridDim.x * gridDim.y * gridDim.z;
+    const unsigned x = (blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) % kArrivalGroups;
+    if (arrived == (G - x + kArrivalGroups - 1) / kArrivalGroups - 1) {
+      unsigned* done = hdr + kHdrLine * (1 + kArrivalGroups);
+      const unsigned groups = G < (unsigned)kArrivalGroups ? G : (unsigned)kArrivalGroups;
+      if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1) {
+        for (int k = 0; k < kArrivalGroups; ++k)
+          __hip_atomic_store(hdr + kHdrLine * (1 + k), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(hdr, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   }
 }
 

@@ -29,7 +29,7 @@ from . import _ops
 
 __all__ = ["HdcMamba9v3Block", "HdcMamba9v3Model", "FusedNormConv1dFunction",
            "fused_norm_conv1d_trainable", "RowLayerNormFunction", "layer_norm", "SlotSsmMixerFunction",
-           "set_differentiable_mixer", "set_fused_out_proj", "BlockState"]
+           "set_differentiable_mixer", "set_fused_out_proj", "set_fused_step_front", "BlockState"]
 
 
 @dataclass
@@ -195,6 +195,11 @@ class HdcMamba9v3Block(nn.Module):
     # workgroups only slow the pre-pass: 25 + 55 us against 24 + 28 us); eager forwards 15.14
     # overlapped against 15.65 in sequence.
     ssm_overlap = "auto"
+    # decode step: the LayerNorm + conv of the token and in_proj as one launch
+    # (hdcm_norm_conv_in_proj_step_fwd: in_proj's weight stream starts while the conv rows are
+    # computed; the same values as the two kernels) where in_proj runs on the wide skinny GEMM
+    # (at least 2048 outputs, d_model <= 2048); set_fused_step_front switches it.
+    fused_step_front = True
 
     def __init__(self, d_model=512, d_state=64, num_heads=8, chunk_size=256, differentiable_mixer=False,
                  fused_out_proj=True):
@@ -451,11 +456,16 @@ class HdcMamba9v3Block(nn.Module):
         dm, ds, H, C = self.d_model, self.d_state, self.num_heads, self.chunk_size
         B = x.shape[0]
         dtype = x.dtype
-        xc = _ops.norm_conv_step(x, self.norm.weight, self.norm.bias, self.conv1d.weight.squeeze(1),
-                                 self.conv1d.bias, self.norm.eps, state.conv)
         w_in, b_in = self.in_proj.weight.to(dtype), self.in_proj.bias.to(dtype)
-        # few rows: the weight-streaming skinny GEMM; otherwise the library GEMM
-        projs = _ops.skinny_linear(xc, w_in, b_in) if _ops.skinny_ok(xc, w_in) else F.linear(xc, w_in, b_in)
+        conv_w = self.conv1d.weight.squeeze(1)
+        if self.fused_step_front and w_in.shape[0] >= 2048 and _ops.norm_conv_in_proj_step_ok(x, w_in):
+            _, projs = _ops.norm_conv_in_proj_step(x, self.norm.weight, self.norm.bias, conv_w, self.conv1d.bias,
+                                                   self.norm.eps, state.conv, w_in, b_in)
+        else:
+            xc = _ops.norm_conv_step(x, self.norm.weight, self.norm.bias, conv_w, self.conv1d.bias, self.norm.eps,
+                                     state.conv)
+            # few rows: the weight-streaming skinny GEMM; otherwise the library GEMM
+            projs = _ops.skinny_linear(xc, w_in, b_in) if _ops.skinny_ok(xc, w_in) else F.linear(xc, w_in, b_in)
         combined = torch.empty(B, ds + dm, device=x.device, dtype=dtype)
         _ops.mixer_step(projs, self.A_log, ds, 3 * ds, self.gamma_buf.to(dtype), self.group_norm.weight,
                         self.group_norm.bias, 1e-5, state.h, state.S_prev, state.S_intra, state.pos, C,
@@ -577,6 +587,15 @@ def set_fused_out_proj(module, enabled=True):
     for m in module.modules():
         if isinstance(m, HdcMamba9v3Block):
             m.fused_out_proj = bool(enabled)
+    return module
+
+
+def set_fused_step_front(module, enabled=True):
+    """Switch the one-launch LayerNorm + conv + in_proj of the decode step of every
+    HdcMamba9v3Block inside ``module`` on or off; returns ``module``."""
+    for m in module.modules():
+        if isinstance(m, HdcMamba9v3Block):
+            m.fused_step_front = bool(enabled)
     return module
 
 

@@ -83,16 +83,20 @@ int hdcm_timed_launch_count(void);
  *    the GPU at once, but at most twice as many, run one round of workgroups, the first ones
  *    taking a second tile, instead of a second round (0 switches it off).  Results do not
  *    depend on it.
+ *  HDCM_OPT_STEP_SPIN_ROUNDS (env HDCM_STEP_SPIN_ROUNDS, default 65536): polling rounds of
+ *    hdcm_norm_conv_in_proj_step_fwd's GEMM workgroups for the conv rows before they count a
+ *    timeout in the workspace header and go on (their outputs are then not valid).
  * hdcm_set_option returns HDCM_EINVAL for an unknown option or a value out of range
- * (0 .. 2^20; SKINNY_COLS8_MAX_N 0 .. 2^30; SKINNY_FOLD_TAIL 0 .. 1); hdcm_get_option returns the current value (0 for an
- * unknown one).
+ * (0 .. 2^20; SKINNY_COLS8_MAX_N 0 .. 2^30; SKINNY_FOLD_TAIL 0 .. 1; STEP_SPIN_ROUNDS 0 .. 2^24);
+ * hdcm_get_option returns the current value (0 for an unknown one).
  * No counterpart in the reference (its launch table, model.py:12-19, is fixed).
  */
 typedef enum {
   HDCM_OPT_SSM_SPIN_ROUNDS = 1,
   HDCM_OPT_SLOT_SEG_TILES = 2,
   HDCM_OPT_SKINNY_COLS8_MAX_N = 3,
-  HDCM_OPT_SKINNY_FOLD_TAIL = 4
+  HDCM_OPT_SKINNY_FOLD_TAIL = 4,
+  HDCM_OPT_STEP_SPIN_ROUNDS = 5
 } hdcm_option;
 int hdcm_set_option(int option, int value);
 int hdcm_get_option(int option);
@@ -347,6 +351,29 @@ int hdcm_skinny_gemm_fwd(const void* A, int64_t a_row_stride, const void* W, int
                          const void* bias, const void* res, int64_t res_row_stride, void* out,
                          int64_t out_row_stride, int64_t M, int64_t N, int64_t K, int dtype,
                          void* stream);
+
+/*
+ * The front of a decode step in one launch: hdcm_norm_conv_step_fwd of x (B rows, D = K
+ * columns; u = its output, hist shifted) followed by hdcm_skinny_gemm_fwd(u, W, bias) into
+ * out [B,N] -- the same values, bit for bit, as those two calls.  The GEMM's weight loads are
+ * issued while the conv rows are computed; its workgroups wait for the rows on flags in the
+ * workspace (ws, at least hdcm_step_workspace_bytes() bytes, 128-byte aligned, zero-filled
+ * before the first call and then kept by the caller for every later call; calls that overlap
+ * on one workspace race).  The 32-bit word at byte 128 of the workspace counts waits that gave
+ * up after HDCM_OPT_STEP_SPIN_ROUNDS polls (0 unless the GPU is shared with work that holds
+ * back the conv rows' workgroups; outputs of such a call are not valid).  bf16 only;
+ * 1 <= B <= 16, D % 32 == 0, D <= 2048; bias may be NULL.
+ * Replaces: the block's norm + conv1d then in_proj of one token (hdcmamba/model.py:22-72
+ * per row, then model.py:313,340); no counterpart as one call (the reference has no decode
+ * step, hdcmamba/train.py:139-151).
+ */
+size_t hdcm_step_workspace_bytes(void);
+int hdcm_norm_conv_in_proj_step_fwd(const void* x, int64_t x_row_stride, const void* ln_w, const void* ln_b,
+                                    const void* conv_w, const void* conv_b, void* hist, float eps, void* u,
+                                    int64_t u_row_stride, const void* W, int64_t w_row_stride,
+                                    const void* bias, void* out, int64_t out_row_stride, int64_t B,
+                                    int64_t D, int64_t N, void* ws, size_t ws_bytes, int dtype,
+                                    void* stream);
 
 /*
  * Tiled bf16 GEMM: out[t,o] = sum_k x[t,k] w[o,k] (+ bias[o]) for t < M, o < N, fp32

@@ -38,7 +38,7 @@ def test_abi_version_and_strerror():
 def test_workspace_sizes():
     lib = _ops.lib()
     # header + (A, H) words of 16 bytes per channel and 512-row tile
-    assert lib.hdcm_ssm_workspace_bytes(1, 32768, 128) == 256 + 128 * 64 * 16
+    assert lib.hdcm_ssm_workspace_bytes(1, 32768, 128) == 2048 + 128 * 64 * 16
     assert lib.hdcm_ssm_workspace_bytes(0, 10, 4) == 0
     n = lib.hdcm_slot_workspace_bytes(1, 32768, 1024, 16, 64, _ops.HDCM_BF16)
     assert n > 0 and n % (2 * 16 * 64 * 64 * 4) == 0
@@ -207,6 +207,39 @@ def test_skinny_gemm_validation():
     assert f(*a) == EALIGN
     a = list(base); a[9] = 0
     assert f(*a) == OK
+
+
+def test_norm_conv_in_proj_step_validation():
+    # hdcm_norm_conv_in_proj_step_fwd(x, x_rs, ln_w, ln_b, conv_w, conv_b, hist, eps, u, u_rs, W, w_rs, bias,
+    #                                 out, o_rs, B, D, N, ws, ws_bytes, dtype, stream)
+    lib = _ops.lib()
+    f = lib.hdcm_norm_conv_in_proj_step_fwd
+    wsb = lib.hdcm_step_workspace_bytes()
+    assert wsb >= 128 * 19  # the tag, the timeouts, 8 flag copies, 9 counters: a 128-byte line each
+    base = [P16, 2048, P16, P16, P16, P16, P16, 1e-5, P16, 2048, P16, 2048, None, P16, 8576, 16, 2048, 8576,
+            P16, wsb, 1, None]
+    a = list(base); a[20] = 0  # fp32 is not built
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[15] = 17  # more than 16 rows
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[15] = 0
+    assert f(*a) == EINVAL
+    a = list(base); a[16] = 2080; a[1] = a[9] = a[11] = 2080  # d_model beyond 2048
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[16] = 2040; a[1] = a[9] = a[11] = 2040  # not a multiple of 32
+    assert f(*a) == EUNSUPPORTED
+    a = list(base); a[18] = None
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[19] = wsb - 4
+    assert f(*a) == EWORKSPACE
+    a = list(base); a[6] = None  # no history
+    assert f(*a) == EINVAL
+    a = list(base); a[14] = 100  # output row shorter than N
+    assert f(*a) == EINVAL
+    a = list(base); a[9] = 2052  # u rows not 16-byte aligned
+    assert f(*a) == EALIGN
+    a = list(base); a[18] = ctypes.c_void_p(16 * 1024 + 64)  # workspace not on a 128-byte line
+    assert f(*a) == EALIGN
 
 
 def test_gemm_validation():

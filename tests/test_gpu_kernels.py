@@ -456,6 +456,84 @@ def test_skinny_fold_tail(dev, M, N, K, bias, res, cols8):
     assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
 
 
+def _front_inputs(B, D, N, bias, seed):
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+    p = dict(ln_w=(1 + 0.1 * torch.randn(D, generator=g)).to(bf), ln_b=(0.1 * torch.randn(D, generator=g)).to(bf),
+             conv_w=(0.3 * torch.randn(D, 4, generator=g)).to(bf), conv_b=(0.1 * torch.randn(D, generator=g)).to(bf),
+             W=(torch.randn(N, D, generator=g) / D ** 0.5).to(bf),
+             b=(0.1 * torch.randn(N, generator=g)).to(bf) if bias else None,
+             hist=(2 * torch.randn(B, 3, D, generator=g) + 0.3).to(bf))
+    xs = [(2 * torch.randn(B, D, generator=g) - 0.4).to(bf) for _ in range(3)]
+    return p, xs
+
+
+@pytest.mark.parametrize("B,D,N,bias", [
+    (16, 2048, 8576, True),   # the d_model 2048 in_proj: 536 tiles, second tiles on the first workgroups
+    (5, 1024, 4480, True),    # d_model 1024: one round of workgroups
+    (1, 768, 3456, False),    # one row, no bias
+    (16, 512, 40000, True),   # more tiles than twice the resident workgroups: several rounds
+    (3, 2048, 2056, True),    # the last tile half full
+])
+def test_norm_conv_in_proj_step(dev, B, D, N, bias):
+    """The one-launch decode front against its two kernels (norm_conv_step, then skinny_linear
+    over its output): the same bits for the conv rows, the projections and the shifted history,
+    over three calls in a row (a new call tag each), with no wait timing out."""
+    _say("norm_conv_in_proj_step", B, D, N, bias)
+    p, xs = _front_inputs(B, D, N, bias, B * 7 + D + N)
+    p = {k: (v.to(dev) if v is not None else None) for k, v in p.items()}
+    h1, h2 = p["hist"].clone(), p["hist"].clone()
+    for x in xs:
+        x = x.to(dev)
+        u1 = _ops.norm_conv_step(x, p["ln_w"], p["ln_b"], p["conv_w"], p["conv_b"], 1e-5, h1)
+        o1 = _ops.skinny_linear(u1, p["W"], p["b"])
+        u2, o2 = _ops.norm_conv_in_proj_step(x, p["ln_w"], p["ln_b"], p["conv_w"], p["conv_b"], 1e-5, h2, p["W"],
+                                             p["b"])
+        torch.cuda.synchronize()
+        assert torch.equal(u1, u2)
+        assert torch.equal(o1, o2)
+        assert torch.equal(h1, h2)
+    assert _ops.step_timeouts(dev) == 0
+    # and against the plain-torch restatement of the projection
+    ref = u2.float().cpu() @ p["W"].float().cpu().t() + (p["b"].float().cpu() if bias else 0)
+    err = (o2.float().cpu() - ref).abs()
+    assert (err <= 2 ** -8 * ref.abs() + 2e-3).all(), f"max err {err.max().item()}"
+
+
+def test_norm_conv_in_proj_step_graph(dev):
+    """The fused front recorded in a HIP graph: every replay (with eager calls of it between the
+    replays, each advancing the call tag) matches the two-kernel path on the same inputs."""
+    _say("norm_conv_in_proj_step graph")
+    B, D, N = 16, 2048, 8576
+    p, xs = _front_inputs(B, D, N, True, 99)
+    p = {k: v.to(dev) for k, v in p.items()}
+    x = xs[0].to(dev)
+    hist = p["hist"].clone()
+    u = torch.empty(B, D, device=dev, dtype=torch.bfloat16)
+    o = torch.empty(B, N, device=dev, dtype=torch.bfloat16)
+    args = (p["ln_w"], p["ln_b"], p["conv_w"], p["conv_b"], 1e-5)
+    _ops.norm_conv_in_proj_step(x, *args, hist, p["W"], p["b"], u=u, out=o)  # the workspace exists before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _ops.norm_conv_in_proj_step(x, *args, hist, p["W"], p["b"], u=u, out=o)
+    g = torch.Generator().manual_seed(5)
+    h_ref = hist.clone()
+    scratch_hist = hist.clone()
+    for rep in range(4):
+        x.copy_((2 * torch.randn(B, D, generator=g)).to(torch.bfloat16))
+        u_ref = _ops.norm_conv_step(x, *args, h_ref)
+        o_ref = _ops.skinny_linear(u_ref, p["W"], p["b"])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(u, u_ref), rep
+        assert torch.equal(o, o_ref), rep
+        assert torch.equal(hist, h_ref), rep
+        _ops.norm_conv_in_proj_step(x, *args, scratch_hist, p["W"], p["b"])  # an eager call between replays
+        torch.cuda.synchronize()
+    assert _ops.step_timeouts(dev) == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("hd,H,two", [(256, 4, True), (160, 3, True), (96, 2, False)])
 def test_gnorm_gate_pass(dev, dtype, hd, H, two):
