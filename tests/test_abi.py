@@ -209,6 +209,22 @@ def test_skinny_gemm_validation():
     assert f(*a) == OK
 
 
+def test_launch_options_round_trip():
+    """Every option the Python wrapper names exists in the library, keeps a value it is set to,
+    rejects values out of range and unknown options (no GPU involved)."""
+    lib = _ops.lib()
+    for name, key in _ops.OPTIONS.items():
+        old = lib.hdcm_get_option(key)
+        assert lib.hdcm_set_option(key, 1) == OK, name
+        assert lib.hdcm_get_option(key) == 1, name
+        assert lib.hdcm_set_option(key, -1) == EINVAL, name
+        assert lib.hdcm_set_option(key, old) == OK, name
+    assert lib.hdcm_set_option(max(_ops.OPTIONS.values()) + 1, 0) == EINVAL
+    assert lib.hdcm_set_option(0, 0) == EINVAL
+    assert lib.hdcm_get_option(99) == 0
+    assert lib.hdcm_set_option(_ops.OPTIONS["skinny_fold_tail"], 2) == EINVAL
+
+
 def test_norm_conv_in_proj_step_validation():
     # hdcm_norm_conv_in_proj_step_fwd(x, x_rs, ln_w, ln_b, conv_w, conv_b, hist, eps, u, u_rs, W, w_rs, bias,
     #                                 out, o_rs, B, D, N, ws, ws_bytes, dtype, stream)
