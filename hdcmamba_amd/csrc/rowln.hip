@@ -21,6 +21,10 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kRows = 4;
+// rowln2_kernel (norm_final then norm_f at the LM's 32768 x 1024 rows) with 2 rows per wave:
+// 23.8-23.9 against 27.0-27.5 us with 4 (35.9 with 8, 24.7-25.2 with 2 rows and 8 waves per
+// workgroup), alternated twice on one box
+constexpr int kRows2 = 2;
 // Below this many rows (decode steps: one row per sequence) every row gets its own
 // single-wave workgroup, so the rows spread over CUs instead of queueing in one wave.
 constexpr int64_t kFewRows = 4096;
@@ -246,7 +250,7 @@ int launch2(const void* in, int64_t in_rs, void* out, int64_t out_rs, const void
     if (rows < kFewRows)
       launch2_shape<T, NG, 1, 1>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
     else
-      launch2_shape<T, NG, kRows, kWavesPerBlock>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
+      launch2_shape<T, NG, kRows2, kWavesPerBlock>(in, in_rs, out, out_rs, w1, b1, eps1, w2, b2, eps2, rows, W, s);
     return hdcm_launch_status();
   });
 }

@@ -81,7 +81,8 @@ class HdcMambaLM(nn.Module):
         """One token per batch row: input_ids [B] -> logits [B,V]; states advance in place."""
         _ops._on_gpu(input_ids)
         with torch.no_grad():
-            return self._logits(self.backbone.step(self.embedding(input_ids), states, pos_dev))
+            # norm_final and norm_f in one pass, then the tied head
+            return self.lm_head(self.backbone.step(self.embedding(input_ids), states, pos_dev, then=self.norm_f))
 
     def capture_decode(self, states):
         """A DecodeGraph stepping ``states`` (as returned by prefill) from replays."""

@@ -573,12 +573,18 @@ class HdcMamba9v3Model(nn.Module):
                             self.norm_final.eps)
         return y, states
 
-    def step(self, x, states, pos_dev=None):
-        """One token per batch row through every block and norm_final: x [B,dm] -> [B,dm]."""
+    def step(self, x, states, pos_dev=None, then=None):
+        """One token per batch row through every block and norm_final: x [B,dm] -> [B,dm].
+        ``then`` (an nn.LayerNorm, the LM's norm_f) is applied after norm_final in the same
+        pass (hdcm_rowln2_fwd, bit-identical to two LayerNorm launches)."""
         with torch.no_grad():
             for layer, st in zip(self.layers, states):
                 x = layer.step(x, st, pos_dev)
-        return _ops.layer_norm(x, self.norm_final.weight, self.norm_final.bias, self.norm_final.eps)
+        nf = self.norm_final
+        if then is not None and _ops.layer_norm2_ok(x):
+            return _ops.layer_norm2(x.contiguous(), nf.weight, nf.bias, nf.eps, then.weight, then.bias, then.eps)
+        x = _ops.layer_norm(x, nf.weight, nf.bias, nf.eps)
+        return x if then is None else _ops.layer_norm(x, then.weight, then.bias, then.eps)
 
 
 def set_fused_out_proj(module, enabled=True):
