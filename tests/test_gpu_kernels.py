@@ -474,6 +474,8 @@ def _front_inputs(B, D, N, bias, seed):
     (1, 768, 3456, False),    # one row, no bias
     (16, 512, 40000, True),   # more tiles than twice the resident workgroups: several rounds
     (3, 2048, 2056, True),    # the last tile half full
+    (2, 32, 20, True),        # one K step (seven of eight waves idle), two tiles, the last one 4 wide
+    (16, 64, 2048, False),    # two K steps, exactly one round
 ])
 def test_norm_conv_in_proj_step(dev, B, D, N, bias):
     """The one-launch decode front against its two kernels (norm_conv_step, then skinny_linear
