@@ -25,7 +25,7 @@
 // Decode is weight- and state-bandwidth bound (the GEMMs around it read every weight once
 // per step), so these kernels are simple: one workgroup per batch row (norm_conv_step) and
 // one per (head, batch) plus one per batch for the SSM channels (mixer_step).  Head dims
-// 32, 64, 96 and 128 are built.
+// are the multiples of 16 up to 128.
 #include "hdcm_common.h"
 
 using namespace hdcm;
