@@ -422,6 +422,101 @@ def cpu_baseline(model, ids_gpu, cfg, runs=3, run_cap_s=90.0):
             "seconds_measured": round(time.perf_counter() - t_start, 2)}
 
 
+def cpu_baseline_block(model, x_gpu, cfg, warmup=3, runs=10):
+    """The CPU oracle's block forward on the same weights and input: ``warmup`` untimed and
+    ``runs`` timed forwards (the reference benchmark's count for single blocks).  ``value``
+    is tokens/s over the mean run."""
+    import torch
+
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    x = x_gpu.cpu()
+    bcfg = oracle.BlockCfg(cfg["d_model"], cfg["d_state"], cfg["num_heads"], cfg["chunk"])
+    t_start = time.perf_counter()
+    for _ in range(warmup):
+        oracle.block_forward(sd, x, bcfg)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        oracle.block_forward(sd, x, bcfg)
+        times.append(time.perf_counter() - t0)
+    mean = sum(times) / len(times)
+    return {"value": round(x.shape[0] * x.shape[1] / mean, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"CPU oracle (plain PyTorch, {str(x.dtype).replace('torch.', '')}) block forward on the same "
+                       f"weights and input, B={x.shape[0]}, L={x.shape[1]}: {warmup} warm-ups, {runs} timed runs"),
+            "cpu_model": _cpu_model(), "run_seconds": [round(t, 3) for t in times],
+            "seconds_measured": round(time.perf_counter() - t_start, 2)}
+
+
+def cpu_baseline_decode(lm, ids_gpu, cfg, L, prefill_layers=2, steps=16):
+    """The CPU oracle on the decode workload's weights: the prefill of ``prefill_layers``
+    blocks at the full B x L timed and extrapolated to every block (marked so), then one
+    warm-up and ``steps`` timed decode steps of the whole model (embedding, every block's
+    recurrent step, final norms, tied head; oracle.block_step).  The decode cost does not
+    depend on the states' values, so blocks past the timed prefill start from zero states of
+    the same shapes.  ``value`` is decode tokens/s (B per step)."""
+    import torch
+
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    F = torch.nn.functional
+    t_start = time.perf_counter()
+    sd = {k: v.detach().cpu() for k, v in lm.state_dict().items()}
+    ids = ids_gpu.cpu()
+    B, n_layers, dm = ids.shape[0], cfg["n_layers"], cfg["d_model"]
+    bcfg = oracle.BlockCfg(dm, cfg["d_state"], cfg["num_heads"], cfg["chunk"])
+    blocks = [{k[len(pre):]: v for k, v in sd.items() if k.startswith(pre)}
+              for pre in (f"backbone.layers.{i}." for i in range(n_layers))]
+    emb = sd["embedding.weight"]
+    steps = min(steps, ids.shape[1] - L - 1)  # token ids past the prefill: a warm-up step, then the timed ones
+    t0 = time.perf_counter()
+    x = F.embedding(ids[:, :L], emb)
+    states = []
+    for i in range(prefill_layers):
+        x, st = oracle.block_prefill_state(blocks[i], x, bcfg)
+        states.append(st)
+        print(f"cpu baseline: prefill block {i} done at {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    t_pre = time.perf_counter() - t0
+    del x
+    H, hd, ds = bcfg.num_heads, bcfg.head_dim, bcfg.d_state
+    for _ in range(prefill_layers, n_layers):
+        states.append({"conv": torch.zeros(B, 3, dm, dtype=emb.dtype), "h": torch.zeros(B, ds),
+                       "S_prev": torch.zeros(B, H, hd, hd), "S_intra": torch.zeros(B, H, hd, hd),
+                       "pos": states[0]["pos"]})
+
+    def step(t):
+        x = F.embedding(ids[:, L + t], emb)
+        for i in range(n_layers):
+            x = oracle.block_step(blocks[i], x, states[i], bcfg)
+        x = F.layer_norm(x.float(), (dm,), sd["backbone.norm_final.weight"].float(),
+                         sd["backbone.norm_final.bias"].float()).to(emb.dtype)
+        x = F.layer_norm(x.float(), (dm,), sd["norm_f.weight"].float(), sd["norm_f.bias"].float()).to(emb.dtype)
+        return F.linear(x, emb)
+
+    step(0)
+    t0 = time.perf_counter()
+    for t in range(1, steps + 1):
+        step(t)
+        if t % 4 == 0:
+            print(f"cpu baseline: decode step {t} at {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    t_dec = time.perf_counter() - t0
+    pre_full = t_pre / prefill_layers * n_layers
+    return {"value": round(B * steps / t_dec, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"CPU oracle (plain PyTorch, bf16) on the same weights: {steps} timed decode steps of the "
+                       f"whole {n_layers}-layer model at B={B} (oracle.block_step per block, final norms, tied "
+                       f"head) after one warm-up step; prefill of {prefill_layers} blocks at B={B}, L={L} timed "
+                       f"and extrapolated to {n_layers} blocks"),
+            "prefill_tokens_per_s": round(B * L / pre_full, 1), "prefill_extrapolated": True,
+            "prefill_seconds_measured": round(t_pre, 2), "decode_seconds": round(t_dec, 2),
+            "cpu_model": _cpu_model(), "seconds_measured": round(time.perf_counter() - t_start, 2)}
+
+
 def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
     """Prefill, then time decode steps (B tokens per step) replayed from the captured graph."""
     B, L = cfg["B"], cfg["L"]
@@ -477,6 +572,7 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
                      "bytes_per_launch": param_bytes + state_bytes},
         "prefill_tokens_per_s": round(B * L / t_prefill, 1),
         "step_front_timeouts": _ops.step_timeouts(dev) if args.fused_step_front == "on" else None,
+        "cpu_baseline": cpu_baseline_decode(lm, ids, cfg, L) if args.cpu_baseline == "on" else None,
         "gpu": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)
@@ -701,8 +797,9 @@ def main():
                            "frac_hbm_peak": round(by / sec_step / 8e12, 4)}
 
     cpu = None
-    if args.cpu_baseline == "on" and args.workload.startswith("lm"):
-        cpu = cpu_baseline(model, inp, cfg, runs=args.cpu_runs)
+    if args.cpu_baseline == "on":
+        cpu = (cpu_baseline(model, inp, cfg, runs=args.cpu_runs) if args.workload.startswith("lm")
+               else cpu_baseline_block(model, inp, cfg))
 
     out = {
         "metric": "forward tokens/sec on 1 MI355X at L=32768; achieved HBM GB/s % of peak",

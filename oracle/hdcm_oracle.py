@@ -39,6 +39,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle_*.py):
 * ``block_forward_stream`` -- pinned: equals ``block_forward`` when the whole sequence is
   the prefill, and row by row equals a sequential recurrence over the padded sequence
   (every stage is causal, so right padding changes no kept row).
+* ``block_prefill_state`` / ``block_step`` -- pinned: a prefill followed by steps equals
+  ``block_forward_stream`` over the same rows (fp32 1e-4, chunk ends and left-padded
+  prefills included); a planted slip in the chunk-end fold fails it.
 * faithful-mode address maps (B1-B3, B5) -- pinned by hand-computed index KATs
   restated from the launch arguments and by the reference's own kernels run under
   Triton's CPU interpreter on the five fp32 block vectors (batch 2, chunk 128, head
@@ -58,7 +61,7 @@ import torch.nn.functional as F
 __all__ = [
     "BlockCfg", "kernel_rounding", "skip_slot_rounding", "SLOT_ROUNDING_SITES", "softplus20", "phi", "norm_conv", "ssm_sequential", "ssm_chunked",
     "slot_sequential", "slot_chunked", "attend_sequential", "attend_chunked", "gnorm_gate", "rowln", "block_forward", "block_forward_stream",
-    "model_forward", "lm_forward", "init_block_params",
+    "block_prefill_state", "block_step", "model_forward", "lm_forward", "init_block_params",
 ]
 
 
@@ -478,6 +481,65 @@ def _block_padded(p, x, cfg, pad, pad_r, semantics, eps, return_states, mixer_gr
     if return_states:
         return out, {"h": h_fin, "S": s_fin, "projs": projs, "combined": combined, "x_conv": x_conv}
     return out
+
+
+def block_prefill_state(p, x, cfg: BlockCfg, eps=1e-5):
+    """block_forward over a prefill x [B,L,D] and the state it leaves for block_step:
+    ``conv`` the last three block-input rows (zero rows before the sequence start, whose
+    LayerNorm is the LN bias as in norm_conv), ``h`` the SSM state, ``S_prev`` the slot state
+    at the chunk boundary the left-padded prefill ends on, ``S_intra`` (unused at offset 0)
+    and the chunk offset ``pos`` = 0.  Returns (out [B,L,D], state)."""
+    out, st = block_forward(p, x, cfg, eps=eps, return_states=True)
+    B, _, D = x.shape
+    H, hd = cfg.num_heads, cfg.head_dim
+    conv = torch.cat([torch.zeros(B, 3, D, dtype=x.dtype), x], 1)[:, -3:].clone()
+    return out, {"conv": conv, "h": st["h"].float().clone(), "S_prev": st["S"].float().clone(),
+                 "S_intra": torch.zeros(B, H, hd, hd), "pos": 0}
+
+
+def block_step(p, x, state, cfg: BlockCfg, eps=1e-5):
+    """One token per batch row after block_prefill_state: x [B,D] -> [B,D], ``state``
+    advanced in place.  The chunked forward continued token by token (what
+    block_forward_stream computes for the whole sequence; the reference has no recurrent
+    step): the conv over the three history rows and the token, the SSM recurrence of
+    ssm_sequential, and for the slot memory, with c the token's offset in its chunk,
+      S_eff = S_prev + phi(k)^T v (c = 0),  gamma S_eff_prev + phi(k)^T v (c > 0),
+      y = phi(q) S_eff,
+    S_eff kept in S_intra between the tokens of a chunk and folded at the chunk's last token
+    into S_prev <- S_eff + (gamma^C - gamma^(C-1)) S_prev = gamma^C S_prev + the chunk's own
+    decayed sum (attend_chunked's running state).  phi(q) and phi(k) are rounded to the
+    activation dtype as in the chunked form; the states stay fp32."""
+    dtype = x.dtype
+    dm, ds, H, C = cfg.d_model, cfg.d_state, cfg.num_heads, cfg.chunk_size
+    hd = cfg.head_dim
+    B = x.shape[0]
+    rows = torch.cat([state["conv"], x[:, None]], 1)  # [B,4,D], oldest first
+    xc = norm_conv(rows, p["norm.weight"], p["norm.bias"], p["conv1d.weight"].squeeze(1),
+                   p["conv1d.bias"], eps)[:, 3]
+    state["conv"] = rows[:, 1:].clone()
+    projs = F.linear(xc, p["in_proj.weight"].to(dtype), p["in_proj.bias"].to(dtype))
+    _, ld, u = _ssm_inputs(projs, p["A_log"].to(dtype), ds)
+    h = state["h"] * torch.exp(ld) + u
+    state["h"] = h
+    off = 3 * ds
+    qf = _rnd(phi(projs[:, off:off + dm].float()), dtype).view(B, H, hd)
+    kf = _rnd(phi(projs[:, off + dm:off + 2 * dm].float()), dtype).view(B, H, hd)
+    v = projs[:, off + 2 * dm:off + 3 * dm].float().view(B, H, hd)
+    g = p["gamma_buf"].to(dtype).float().view(1, H, 1, 1)
+    c = state["pos"]
+    kv = kf[..., :, None] * v[..., None, :]
+    S_eff = state["S_prev"] + kv if c == 0 else g * state["S_intra"] + kv
+    y = (qf[..., :, None] * S_eff).sum(-2)  # [B,H,hd]
+    if c == C - 1:
+        state["S_prev"] = S_eff + (g ** C - g ** (C - 1)) * state["S_prev"]
+    else:
+        state["S_intra"] = S_eff
+    state["pos"] = (c + 1) % C
+    gate = projs[:, off + 3 * dm:]
+    gg = gnorm_gate(y.view(B, 1, H, hd), gate.view(B, 1, dm), p["group_norm.weight"], p["group_norm.bias"], H)
+    combined = torch.cat([_rnd(h, dtype), _rnd(gg[:, 0], dtype)], -1).to(dtype)
+    cn = F.layer_norm(combined.float(), (ds + dm,)).to(dtype)
+    return x + F.linear(cn, p["out_proj.weight"].to(dtype))
 
 
 def _sub(sd, prefix):

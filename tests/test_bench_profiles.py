@@ -57,3 +57,28 @@ def test_stats_summary_lines(tmp_path):
     text = bench.stats_summary(path)
     assert "avg_us: norm_conv 29.5" in text
     assert text.splitlines()[0].startswith(bench.SOURCE_KEY)
+
+
+def test_cpu_baselines_of_the_block_and_decode_workloads():
+    """The CPU-baseline legs of the block and decode workloads on a tiny model (CPU tensors,
+    no GPU): they run the oracle's block forward, prefill and recurrent steps and report
+    tokens/s with the sample they timed."""
+    import torch
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from cfgs import make_lm  # noqa: E402
+    from hdcmamba_amd import HdcMamba9v3Block
+
+    torch.manual_seed(0)
+    blk = HdcMamba9v3Block(64, 16, 4, 8).to(torch.bfloat16)
+    x = torch.randn(2, 24, 64).to(torch.bfloat16)
+    cfg = {"d_model": 64, "d_state": 16, "num_heads": 4, "chunk": 8}
+    r = bench.cpu_baseline_block(blk, x, cfg, warmup=1, runs=2)
+    assert r["value"] > 0 and r["kind"] == "port" and len(r["run_seconds"]) == 2 and "B=2, L=24" in r["sample"]
+
+    lm = make_lm("lm_c3", n_layers=2).to(torch.bfloat16)
+    ids = torch.randint(0, 50304, (2, 16 + 4))
+    cfg = {"d_model": 768, "d_state": 64, "num_heads": 12, "chunk": 64, "n_layers": 2}
+    r = bench.cpu_baseline_decode(lm, ids, cfg, L=16, prefill_layers=1, steps=16)
+    assert r["value"] > 0 and r["prefill_extrapolated"] and r["prefill_tokens_per_s"] > 0
+    assert "3 timed decode steps" in r["sample"]  # capped by the ids past the prefill

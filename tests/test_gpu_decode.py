@@ -60,6 +60,37 @@ def test_block_prefill_then_steps(dev, dtype, B, dm, ds, H, C, n_pre, n_dec):
     assert st.pos == (n_pre + (C - n_pre % C) % C + n_dec) % C
 
 
+@pytest.mark.parametrize("dtype,B,dm,ds,H,C,n_pre,n_dec", [
+    (torch.float32, 2, 256, 64, 8, 16, 40, 30), (torch.bfloat16, 2, 512, 128, 8, 64, 130, 70),
+    (torch.bfloat16, 16, 2048, 128, 32, 64, 128, 66)])  # C5 width (fused decode front)
+def test_block_steps_and_states_match_oracle_step(dev, dtype, B, dm, ds, H, C, n_pre, n_dec):
+    """The GPU prefill's carried state and every decode step against the oracle's recurrent
+    step (oracle.block_prefill_state / block_step), which uses the step's own rounding points:
+    outputs per token and, after the last step, the conv history, the SSM state and both slot
+    states (S_intra compared where it is live, i.e. off a chunk boundary)."""
+    _say("block steps vs oracle step", dtype, B, dm, ds, H, C, n_pre, n_dec)
+    blk = _block(dm, ds, H, C, dtype, seed=n_pre + dm + 1)
+    x = torch.randn(B, n_pre + n_dec, dm, generator=torch.Generator().manual_seed(dm + 7)).to(dtype)
+    cfg = oracle_cfg(blk)
+    sd = _sd(blk)
+    y0_ref, ost = oracle.block_prefill_state(sd, x[:, :n_pre], cfg)
+    refs = [oracle.block_step(sd, x[:, n_pre + t], ost, cfg) for t in range(n_dec)]
+    blk = blk.to(dev)
+    xd = x.to(dev)
+    with torch.no_grad():
+        y0, st = blk.prefill(xd[:, :n_pre])
+        assert_close(st.conv, x[:, n_pre - 3:n_pre], dtype, "prefill conv history")
+        ys = [blk.step(xd[:, n_pre + t].contiguous(), st) for t in range(n_dec)]
+    assert_close(y0, y0_ref, dtype, "prefill rows")
+    assert_close(torch.stack(ys, 1), torch.stack(refs, 1), dtype, "decode rows")
+    assert st.pos == ost["pos"]
+    assert torch.equal(st.conv.cpu(), ost["conv"])
+    assert_close_normwise(st.h, ost["h"], dtype, "SSM state")
+    assert_close_normwise(st.S_prev, ost["S_prev"], dtype, "slot state at the chunk boundary")
+    if ost["pos"] != 0:
+        assert_close_normwise(st.S_intra, ost["S_intra"], dtype, "slot state inside the chunk")
+
+
 @pytest.mark.parametrize("B,n_pre,n_dec", [(2, 8192, 32), (16, 8192, 8)])
 def test_block_c5_width_prefill_then_steps(dev, B, n_pre, n_dec):
     """A block of the 48-layer d_model 2048 decode workload (32 heads, d_state 128, chunk 64)

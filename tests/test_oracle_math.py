@@ -281,6 +281,42 @@ def test_stream_equals_sequential_recurrence(n_prefill):
         assert (oracle.block_forward(p, x, cfg) - got).abs().max() > 1e-4
 
 
+@pytest.mark.parametrize("n_prefill,C,H", [(8, 4, 2), (5, 4, 2), (1, 4, 4), (9, 3, 2), (6, 1, 2)])
+def test_block_step_equals_stream(n_prefill, C, H):
+    """block_prefill_state then block_step token by token equals block_forward_stream over
+    the same rows: chunk ends inside the steps, left-padded prefills, one-row chunks."""
+    cfg = oracle.BlockCfg(16, 4, H, C)
+    p = oracle.init_block_params(cfg, generator_seed=6 + C)
+    n_dec = 11
+    x = torch.randn(2, n_prefill + n_dec, 16, generator=_g(12 + n_prefill))
+    ref = oracle.block_forward_stream(p, x, cfg, n_prefill)
+    y0, st = oracle.block_prefill_state(p, x[:, :n_prefill], cfg)
+    torch.testing.assert_close(y0, ref[:, :n_prefill], atol=1e-5, rtol=1e-5)
+    ys = [oracle.block_step(p, x[:, t], st, cfg) for t in range(n_prefill, n_prefill + n_dec)]
+    torch.testing.assert_close(torch.stack(ys, 1), ref[:, n_prefill:], atol=1e-4, rtol=1e-4)
+    assert st["pos"] == (n_prefill + (C - n_prefill % C) % C + n_dec) % C
+
+
+def test_block_step_chunk_end_fold_is_needed():
+    """Dropping the (gamma^C - gamma^(C-1)) S_prev term of the chunk-end fold (planted in the
+    state after the first chunk end) makes the continuation miss the stream form."""
+    cfg = oracle.BlockCfg(16, 4, 2, 4)
+    p = oracle.init_block_params(cfg, generator_seed=21)
+    x = torch.randn(2, 8 + 9, 16, generator=_g(22))
+    ref = oracle.block_forward_stream(p, x, cfg, 8)
+    _, st = oracle.block_prefill_state(p, x[:, :8], cfg)
+    g = p["gamma_buf"].float().view(1, 2, 1, 1)
+    ys, planted = [], False
+    for t in range(8, 17):
+        c, s_prev = st["pos"], st["S_prev"].clone()
+        ys.append(oracle.block_step(p, x[:, t], st, cfg))
+        if c == 3 and not planted:
+            st["S_prev"] = st["S_prev"] - (g ** 4 - g ** 3) * s_prev
+            planted = True
+    assert planted
+    assert (torch.stack(ys, 1) - ref[:, 8:]).abs().max() > 1e-3
+
+
 # ----------------------------------------------------------------------------- norm_conv gradients
 def _norm_conv_library(x, w, b, cw, cb, eps):
     """LayerNorm then depthwise conv1d through PyTorch's own modules, the three rows before
