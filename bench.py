@@ -9,7 +9,7 @@ with tokens/s, the roofline of the dominant custom kernel (HIP events recorded b
 custom kernel's own dispatch, over a second timed region of eager forwards), per-kernel
 figures, and the CPU oracle's throughput on a bounded sample of the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c2|lm_c5_decode|lm_c4_train]
+    python bench.py [--steps K] [--warmup W] [--workload lm_c4|lm_c3|block_c1|block_c2|lm_c5_decode|lm_c4_train]
                     [--graph on|off] [--tuned-gemms on|off] [--cpu-baseline on|off]
 """
 from __future__ import annotations
@@ -635,7 +635,7 @@ def main():
     ap.add_argument("--differentiable-mixer", action="store_true",
                     help="lm_c4_train: train the SSM, slot and gate parameters too")
     ap.add_argument("--workload", default="lm_c4",
-                    choices=["lm_c4", "lm_c3", "block_c2", "lm_c5_decode", "lm_c4_train"],
+                    choices=["lm_c4", "lm_c3", "block_c1", "block_c2", "lm_c5_decode", "lm_c4_train"],
                     help="lm_c5_decode: 48-layer d_model=2048 LM, prefill B=16 x 8192, then timed "
                          "single-token decode steps (a separate measurement, not the headline line)")
     ap.add_argument("--eager", action="store_true", help="lm_c5_decode: step from Python instead of "
