@@ -24,10 +24,10 @@
 // start; each workgroup then counts itself in one of eight counters of the header (an atomic
 // whose latency hides behind its loads; the workgroup that completes a counter counts it in a
 // ninth), and the last to arrive advances the epoch when it ends (every workgroup has read the
-// tag by then, and nothing reads the header again in this call), so the workspace never needs
-// clearing.  The tag and the counters sit on 128-byte lines of their own: one counter on the
-// tag's line took every workgroup's arrival in turn, ~1 us of the scan at 256 workgroups
-// (it must be zero before its first use).  A workgroup that finds an earlier total missing
+// tag by then, and nothing reads the header again in this call), so the workspace needs
+// clearing only once, before its first use.  The tag and the counters sit on 128-byte lines of
+// their own: one counter on the tag's line took every workgroup's arrival in turn, ~1 us of the
+// scan at 256 workgroups.  A workgroup that finds an earlier total missing
 // polls for a bounded number of rounds, then computes that tile's total itself with the
 // same code and publishes it on the owner's behalf (identical bits), so no wait is unbounded
 // whatever order the workgroups run in.  With row_stats the workgroup also writes, per row,
