@@ -48,6 +48,12 @@ Parity status of each function (how it is pinned, see tests/test_oracle_*.py):
   dim 96, ragged length 100): the faithful oracle matches them within 5e-4 normwise,
   the intended semantics miss every one by more than 1e-2.  The reference is never run
   on a GPU (it needs CUDA).
+* ``model_forward`` -- pinned: the reference's own model forward (two fp32 blocks at chunk
+  64, head dim 32, under Triton's CPU interpreter) matches the faithful oracle within 2e-8;
+  the blocks in the other order, or without norm_final, miss it.
+* ``lm_forward`` -- by construction: embedding, ``model_forward``, norm_f and the tied head
+  (F.embedding, F.layer_norm, F.linear); the reference's LM wrapper cannot be imported here
+  (train_fineweb.py needs wandb).
 * constructor RNG order -- pinned by the fixture in tests/golden (see its script).
 """
 from __future__ import annotations

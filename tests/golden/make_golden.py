@@ -1,8 +1,9 @@
 """Write golden vectors by running the reference implementation itself.
 
 Runs N01N9/hdcmamba's own code (hdcmamba/model.py: its constructor, the
-FusedNormConv1dFunction path and the full HdcMamba9v3Block forward with its Triton
-kernels executed by Triton's CPU interpreter, TRITON_INTERPRET=1) on small seeded
+FusedNormConv1dFunction path, the full HdcMamba9v3Block forward and a two-block
+HdcMamba9v3Model forward with its Triton kernels executed by Triton's CPU interpreter,
+TRITON_INTERPRET=1) on small seeded
 inputs, and saves inputs, weights, captured intermediates and outputs as plain tensor
 files (torch.save of dicts of tensors; load with weights_only=True).  Nothing of the
 reference's code is copied into the fixtures: they hold data only.
@@ -144,6 +145,32 @@ def main(ref_root: str) -> None:
                                 D_STATE=ds, CHUNK_SIZE=C, BLOCK_SIZE_D=64)
         out[f"ssm_{dt_name}"] = {"args": torch.tensor([B, L, ds, C]), "projs": projs, "A_log": A_log,
                                  "y": y.view(B, L, ds).clone()}
+
+    # 5. The model forward (model.py:396-404): two blocks chained through the residual stream,
+    #    then norm_final, fp32.  The reference's model builds its blocks with chunk 256, which
+    #    its slot kernels cannot run (model.py:17,245-246: rows past the 128-row tile are never
+    #    written), so the blocks are switched to chunk 64 before the forward.
+    from hdcmamba.model import HdcMamba9v3Model
+    torch.manual_seed(300)
+    m = HdcMamba9v3Model(d_model=64, n_layers=2, d_state=16, num_slots=32, num_heads=2)
+    g = torch.Generator().manual_seed(301)
+    with torch.no_grad():
+        for blk in m.layers:
+            blk.chunk_size = 64
+            blk.group_norm.weight.copy_(1 + 0.1 * torch.randn(64, generator=g))
+            blk.decay_log.copy_(torch.log(1.0 / (0.9 + 0.09 * torch.rand(2, generator=g)) - 1.0))
+            blk.gamma_buf.copy_(torch.exp(-torch.nn.functional.softplus(blk.decay_log)))
+        m.norm_final.weight.copy_(1 + 0.1 * torch.randn(64, generator=g))
+        m.norm_final.bias.copy_(0.1 * torch.randn(64, generator=g))
+    m = m.eval()
+    for blk in m.layers:
+        blk.triton_cfg = cfg_for(blk)
+    x = torch.randn(1, 100, 64, generator=g)
+    with torch.no_grad():
+        y = m(x)
+    out["model_2l"] = {"args": torch.tensor([64, 16, 2, 64, 1, 100, 2]), "x": x, "y": y,
+                       **{"p." + k: v.detach().clone() for k, v in m.state_dict().items()}}
+    print("model_2l done", flush=True)
 
     path = HERE / "reference_vectors.pt"
     torch.save(out, path)

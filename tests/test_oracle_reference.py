@@ -156,3 +156,25 @@ def test_intended_departs_from_reference(vectors, name):
     gap = _rel(y, v["y"])
     print(f"{name}: intended vs reference kernels, normwise {gap:.3f}")
     assert gap > 1e-2
+
+
+def test_model_forward_matches_reference(vectors):
+    """oracle.model_forward (the blocks chained through the residual stream, then norm_final)
+    against the reference's own HdcMamba9v3Model forward (two fp32 blocks at chunk 64, head
+    dim 32): the faithful oracle matches it, and neither the blocks in the other order nor the
+    blocks without norm_final do."""
+    v = vectors["model_2l"]
+    dm, ds, H, C, B, L, n_layers = v["args"].tolist()
+    sd = _params(v)
+    cfg = BlockCfg(dm, ds, H, C)
+    with oracle.kernel_rounding("trunc"):
+        y = oracle.model_forward(sd, v["x"], cfg, n_layers, "faithful")
+        swapped = oracle.model_forward(sd, v["x"], cfg, n_layers, "faithful", layers=[1, 0])
+        x = v["x"]
+        for i in range(n_layers):
+            pre = f"layers.{i}."
+            x = oracle.block_forward({k[len(pre):]: t for k, t in sd.items() if k.startswith(pre)}, x, cfg,
+                                     "faithful")
+    assert _rel(y, v["y"]) < 5e-4
+    assert _rel(swapped, v["y"]) > 1e-2
+    assert _rel(x, v["y"]) > 1e-2
