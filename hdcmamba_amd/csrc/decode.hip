@@ -257,9 +257,17 @@ __global__ __launch_bounds__(kThreads) void mixer_step_kernel(
 #pragma unroll
     for (int k = 0; k < RGS; ++k) y += sy[k][tid];
   }
-  // GroupNorm over the head's hd values, then the gate
+  // GroupNorm over the head's hd values, then the gate.  Up to 64 values they are all in wave 0,
+  // whose own sums are the workgroup's (the other waves add zeros), so the other waves are done
+  // and no barrier is needed.
   float st[2] = {tid < HD ? y : 0.f, tid < HD ? y * y : 0.f};
-  block_sum<2>(st, red);
+  if constexpr (HD <= kWave) {
+    if (tid >= kWave) return;
+    st[0] = wave_sum(st[0]);
+    st[1] = wave_sum(st[1]);
+  } else {
+    block_sum<2>(st, red);
+  }
   const float mean = st[0] / (float)HD;
   const float var = fmaxf(st[1] / (float)HD - mean * mean, 0.f);
   const float rinv = rsqrtf(var + gn_eps);
