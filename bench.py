@@ -546,6 +546,15 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
             step(tok)
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
+        # Per-kernel durations of the step's custom kernels: HIP events from their own dispatch
+        # timestamps over a few eager steps (launches inside a graph replay carry no events).
+        step_kernels = ("norm_conv_in_proj_step", "norm_conv_step", "skinny_gemm", "mixer_step", "rowln_gemm")
+        _ops.timer.active = set(step_kernels)
+        for t in range(min(8, steps)):
+            lm.step(toks[t], states)
+        torch.cuda.synchronize()
+        _ops.timer.active = set()
+        step_times = _ops.timer.collect()
     # bytes one step must move: every parameter once (the tied head counted once) plus the
     # carried states: slot, one fp32 state read and one written per token (S_intra between the
     # tokens of a chunk, S_prev at its first and last), plus S_prev read again at a chunk's
@@ -558,6 +567,26 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
                                  + 2 * st.conv.numel() * 2)
     ms = sec / steps * 1e3
     gbs = (param_bytes + state_bytes) / (ms * 1e-3) / 1e9
+    # per layer: the front streams the in_proj weight, the mixer reads and writes one fp32 slot
+    # state per (sequence, head), out_proj streams its weight (the rows they read and write
+    # are a few hundred KB)
+    dm, ds, H = cfg["d_model"], cfg["d_state"], cfg["num_heads"]
+    hd = dm // H
+    P = 3 * ds + 4 * dm
+    step_bytes = {"norm_conv_in_proj_step": P * dm * 2, "mixer_step": 2 * B * H * hd * hd * 4,
+                  "rowln_gemm": dm * (ds + dm) * 2}
+    step_kernel_table = {}
+    for name, calls in step_times.items():
+        flat = [k[0] for k in calls if k]
+        if not flat:
+            continue
+        us = _mean(flat) * 1e3
+        entry = {"us": round(us, 2), "launches": len(flat)}
+        if name in step_bytes:
+            g = step_bytes[name] / (us * 1e-6) / 1e9
+            entry.update(bytes_per_launch=step_bytes[name], bound="hbm", **{"GB/s": round(g, 1)},
+                         frac=round(g / HBM_PEAK_GBS, 4))
+        step_kernel_table[name] = entry
     out = {
         "metric": "decode tokens/sec on 1 MI355X, B=16 after an L=8192 prefill",
         "value": round(B * steps / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -571,6 +600,11 @@ def decode_bench(args, torch, cfg, make_lm, lm_input, dev):
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": param_bytes + state_bytes},
         "prefill_tokens_per_s": round(B * L / t_prefill, 1),
+        "kernels": step_kernel_table,
+        "kernel_timing": ("HIP events from each custom kernel's own dispatch timestamps over eager decode "
+                          "steps after the timed replays (norm_conv_in_proj_step: the LayerNorm + conv + "
+                          "in_proj front; mixer_step; rowln_gemm: out_proj with the folded LayerNorm and "
+                          "the residual); mean per launch; bytes: the streamed weight or the slot states"),
         "step_front_timeouts": _ops.step_timeouts(dev) if args.fused_step_front == "on" else None,
         "cpu_baseline": cpu_baseline_decode(lm, ids, cfg, L) if args.cpu_baseline == "on" else None,
         "gpu": torch.cuda.get_device_name(0),
